@@ -1,0 +1,273 @@
+// Thin torch binding over libgdn_amd.so's C ABI.
+//
+// Exposes four submodules with the reference's pybind API (names, positional
+// argument order, dtypes, return conventions), so a caller written against the
+// reference's torch.utils.cpp_extension.load() modules works unchanged:
+//   prefill.prefill(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale)
+//       -> (out bf16 [B,H,T,V], state_out fp32 [B,H,K,V])
+//       + attrs H_DIM K_DIM V_DIM C_DIM     (kernels/prefill_chunked.cu:422-527)
+//   decode.forward(q, k, v, a, b, A_log, dt_bias, S_in, scale, o_out, S_out)
+//                                           (kernels/decode.cu:172-218)
+//   rmsnorm.forward(x, gamma, eps, block_threads, rows_per_block) -> y
+//                                           (kernels/rmsnorm.cu:133-153,278-298)
+//   proj.forward(input, weight, conv_w) -> out (kernels/fused_proj_conv_silu.cu:298-361)
+// Errors surface as RuntimeError, like the reference's TORCH_CHECK.  Launches
+// go to torch's current HIP stream of the tensors' device.
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include "../../include/gdn_amd.h"
+
+namespace {
+
+using at::Tensor;
+
+void* stream_of(const Tensor& t) {
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+#define GDN_CHECK_STATUS(call, who)                                                    \
+    do {                                                                                \
+        const int _st = (call);                                                         \
+        TORCH_CHECK(_st == GDN_OK, who, ": ", gdn_status_string(_st), ": ", gdn_last_error()); \
+    } while (0)
+
+void check_gpu(const Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+void check_bf16(const Tensor& t, const char* name) {
+    check_gpu(t, name);
+    TORCH_CHECK(t.scalar_type() == at::kBFloat16, name, " must be bfloat16");
+}
+
+void check_f32(const Tensor& t, const char* name) {
+    check_gpu(t, name);
+    TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be float32");
+}
+
+const gdn_bf16_t* bf(const Tensor& t) { return reinterpret_cast<const gdn_bf16_t*>(t.data_ptr()); }
+gdn_bf16_t* bf_mut(const Tensor& t) { return reinterpret_cast<gdn_bf16_t*>(t.data_ptr()); }
+
+// ---------------------------------------------------------------------------
+// prefill
+// ---------------------------------------------------------------------------
+std::tuple<Tensor, Tensor> prefill(Tensor q, Tensor k, Tensor v, Tensor A_log, Tensor a, double dt_bias,
+                                   Tensor b_logits, Tensor mask, Tensor state_in, double scale) {
+    check_bf16(q, "q");
+    check_bf16(k, "k");
+    check_bf16(v, "v");
+    check_bf16(a, "a");
+    check_bf16(b_logits, "b_logits");
+    check_f32(A_log, "A_log");
+    TORCH_CHECK(q.dim() == 4 && k.sizes() == q.sizes(), "q, k must be [B, H, T, K] of equal shape");
+    const int64_t B = q.size(0), H = q.size(1), T = q.size(2), K = q.size(3);
+    TORCH_CHECK(v.dim() == 4 && v.size(0) == B && v.size(1) == H && v.size(2) == T, "v must be [B, H, T, V]");
+    const int64_t V = v.size(3);
+    TORCH_CHECK(a.dim() == 3 && a.size(0) == B && a.size(1) == H && a.size(2) == T, "a must be [B, H, T]");
+    TORCH_CHECK(b_logits.sizes() == a.sizes(), "b_logits must be [B, H, T]");
+    TORCH_CHECK(A_log.numel() == H, "A_log must have H entries");
+    const float* mask_ptr = nullptr;
+    if (mask.defined() && mask.numel() > 0) {
+        check_f32(mask, "mask");
+        TORCH_CHECK(mask.dim() == 2 && mask.size(0) == B && mask.size(1) == T, "mask must be [B, T]");
+        mask_ptr = mask.data_ptr<float>();
+    }
+    const float* sin_ptr = nullptr;
+    if (state_in.defined() && state_in.numel() > 0) {
+        check_f32(state_in, "state_in");
+        TORCH_CHECK(state_in.dim() == 4 && state_in.size(0) == B && state_in.size(1) == H &&
+                        state_in.size(2) == K && state_in.size(3) == V,
+                    "state_in must be [B, H, K, V] or empty");
+        sin_ptr = state_in.data_ptr<float>();
+    }
+    const c10::DeviceGuard guard(q.device());
+    auto out = at::empty({B, H, T, V}, q.options());
+    auto state_out = at::empty({B, H, K, V}, q.options().dtype(at::kFloat));
+    const size_t ws_bytes = gdn_prefill_workspace_bytes(B, H, T, K, V);
+    auto ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+    GDN_CHECK_STATUS(gdn_prefill_hip(bf(q), bf(k), bf(v), A_log.data_ptr<float>(), bf(a), static_cast<float>(dt_bias),
+                                     bf(b_logits), mask_ptr, sin_ptr, static_cast<float>(scale), bf_mut(out),
+                                     state_out.data_ptr<float>(), B, H, T, K, V, ws.data_ptr(), ws_bytes,
+                                     stream_of(q)),
+                     "prefill");
+    return {out, state_out};
+}
+
+// Packed variable-length prefill (no reference counterpart).
+// q, k [1, H, Ttot, K]; v [1, H, Ttot, V]; a, b_logits [1, H, Ttot];
+// cu_seqlens int32/int64 [N+1] on CPU or GPU; state_in [N, H, K, V] or empty.
+std::tuple<Tensor, Tensor> prefill_varlen(Tensor q, Tensor k, Tensor v, Tensor A_log, Tensor a, double dt_bias,
+                                          Tensor b_logits, Tensor cu_seqlens, Tensor state_in, double scale,
+                                          std::optional<Tensor> mask_opt, int64_t max_seqlen) {
+    check_bf16(q, "q");
+    check_bf16(k, "k");
+    check_bf16(v, "v");
+    check_bf16(a, "a");
+    check_bf16(b_logits, "b_logits");
+    check_f32(A_log, "A_log");
+    TORCH_CHECK(q.dim() == 4 && q.size(0) == 1 && k.sizes() == q.sizes(), "q, k must be [1, H, T_total, K]");
+    const int64_t H = q.size(1), Ttot = q.size(2), K = q.size(3);
+    TORCH_CHECK(v.dim() == 4 && v.size(0) == 1 && v.size(1) == H && v.size(2) == Ttot, "v must be [1, H, T_total, V]");
+    const int64_t V = v.size(3);
+    TORCH_CHECK(a.dim() == 3 && a.size(0) == 1 && a.size(1) == H && a.size(2) == Ttot, "a must be [1, H, T_total]");
+    TORCH_CHECK(b_logits.sizes() == a.sizes(), "b_logits must be [1, H, T_total]");
+    TORCH_CHECK(A_log.numel() == H, "A_log must have H entries");
+    TORCH_CHECK(cu_seqlens.dim() == 1 && cu_seqlens.numel() >= 2, "cu_seqlens must be [N + 1]");
+    const int64_t N = cu_seqlens.numel() - 1;
+    // Validate offsets on the host (one small copy): kernels index with them.
+    auto cu_host = cu_seqlens.to(at::kCPU).to(at::kLong).contiguous();
+    const int64_t* cu = cu_host.data_ptr<int64_t>();
+    TORCH_CHECK(cu[0] == 0 && cu[N] == Ttot, "cu_seqlens must start at 0 and end at T_total");
+    int64_t maxlen = 0;
+    for (int64_t i = 0; i < N; ++i) {
+        TORCH_CHECK(cu[i + 1] >= cu[i], "cu_seqlens must be non-decreasing");
+        maxlen = std::max(maxlen, cu[i + 1] - cu[i]);
+    }
+    if (max_seqlen > 0) TORCH_CHECK(max_seqlen >= maxlen, "max_seqlen is smaller than a sequence");
+    const float* mask_ptr = nullptr;
+    const Tensor mask = mask_opt.has_value() ? *mask_opt : Tensor();
+    if (mask.defined() && mask.numel() > 0) {
+        check_f32(mask, "mask");
+        TORCH_CHECK(mask.numel() == Ttot, "mask must have T_total entries");
+        mask_ptr = mask.data_ptr<float>();
+    }
+    const float* sin_ptr = nullptr;
+    if (state_in.defined() && state_in.numel() > 0) {
+        check_f32(state_in, "state_in");
+        TORCH_CHECK(state_in.dim() == 4 && state_in.size(0) == N && state_in.size(1) == H &&
+                        state_in.size(2) == K && state_in.size(3) == V,
+                    "state_in must be [N, H, K, V] or empty");
+        sin_ptr = state_in.data_ptr<float>();
+    }
+    const c10::DeviceGuard guard(q.device());
+    auto cu_dev = cu_host.to(at::kInt).to(q.device());
+    auto out = at::empty({1, H, Ttot, V}, q.options());
+    auto state_out = at::empty({N, H, K, V}, q.options().dtype(at::kFloat));
+    const size_t ws_bytes = gdn_prefill_varlen_workspace_bytes(N, H, Ttot, K, V);
+    auto ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+    GDN_CHECK_STATUS(gdn_prefill_varlen_hip(bf(q), bf(k), bf(v), A_log.data_ptr<float>(), bf(a),
+                                            static_cast<float>(dt_bias), bf(b_logits), mask_ptr,
+                                            cu_dev.data_ptr<int32_t>(), N, static_cast<int>(maxlen), sin_ptr,
+                                            static_cast<float>(scale), bf_mut(out), state_out.data_ptr<float>(), H,
+                                            Ttot, K, V, ws.data_ptr(), ws_bytes, stream_of(q)),
+                     "prefill_varlen");
+    return {out, state_out};
+}
+
+// ---------------------------------------------------------------------------
+// decode
+// ---------------------------------------------------------------------------
+void decode_forward(Tensor q, Tensor k, Tensor v, Tensor a, Tensor b, Tensor A_log, Tensor dt_bias, Tensor S_in,
+                    double scale, Tensor o_out, Tensor S_out) {
+    check_bf16(q, "q");
+    check_bf16(k, "k");
+    check_bf16(v, "v");
+    check_bf16(a, "a");
+    check_bf16(b, "b");
+    check_f32(A_log, "A_log");
+    check_f32(dt_bias, "dt_bias");
+    check_f32(S_in, "S_in");
+    check_f32(o_out, "o_out");
+    check_f32(S_out, "S_out");
+    TORCH_CHECK(q.dim() == 3 && k.sizes() == q.sizes(), "q, k must be [B, H, K]");
+    const int64_t B = q.size(0), H = q.size(1), K = q.size(2);
+    TORCH_CHECK(v.dim() == 3 && v.size(0) == B && v.size(1) == H, "v must be [B, H, V]");
+    const int64_t V = v.size(2);
+    TORCH_CHECK(a.numel() == B * H && b.numel() == B * H, "a, b must be [B, H]");
+    TORCH_CHECK(A_log.numel() == H && dt_bias.numel() == H, "A_log, dt_bias must be [H]");
+    TORCH_CHECK(S_in.numel() == B * H * K * V && S_out.numel() == B * H * K * V, "S_in, S_out must be [B, H, K, V]");
+    TORCH_CHECK(o_out.numel() == B * H * V, "o_out must be [B, H, V]");
+    const c10::DeviceGuard guard(q.device());
+    GDN_CHECK_STATUS(gdn_decode_hip(bf(q), bf(k), bf(v), bf(a), bf(b), A_log.data_ptr<float>(),
+                                    dt_bias.data_ptr<float>(), S_in.data_ptr<float>(), static_cast<float>(scale),
+                                    o_out.data_ptr<float>(), S_out.data_ptr<float>(), B, H, K, V, stream_of(q)),
+                     "decode");
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm
+// ---------------------------------------------------------------------------
+Tensor rmsnorm_forward(Tensor x, Tensor gamma, double eps, int64_t block_threads, int64_t rows_per_block) {
+    // Launch-shape arguments are validated with the reference's rules
+    // (kernels/rmsnorm.cu:140-151); the kernel picks its own shape.
+    TORCH_CHECK(rows_per_block >= 1, "rows_per_block must be >= 1");
+    TORCH_CHECK(block_threads >= 32, "block_threads must be >= 32");
+    TORCH_CHECK(block_threads <= 1024, "block_threads must be <= 1024");
+    TORCH_CHECK(block_threads % rows_per_block == 0, "block_threads must be divisible by rows_per_block");
+    const int64_t tpr = block_threads / rows_per_block;
+    TORCH_CHECK(tpr >= 32, "threads_per_row must be >= 32");
+    TORCH_CHECK(tpr % 32 == 0, "threads_per_row must be a multiple of 32");
+    check_bf16(x, "x");
+    check_bf16(gamma, "gamma");
+    TORCH_CHECK(x.dim() == 2, "x must be [R, D]");
+    TORCH_CHECK(gamma.dim() == 1 && gamma.size(0) == x.size(1), "gamma must be [D]");
+    TORCH_CHECK(x.get_device() == gamma.get_device(), "x and gamma must be on the same device");
+    const c10::DeviceGuard guard(x.device());
+    auto y = at::empty_like(x);
+    GDN_CHECK_STATUS(gdn_rmsnorm_hip(bf(x), bf(gamma), bf_mut(y), x.size(0), x.size(1), static_cast<float>(eps),
+                                     stream_of(x)),
+                     "rmsnorm");
+    return y;
+}
+
+// ---------------------------------------------------------------------------
+// proj
+// ---------------------------------------------------------------------------
+Tensor proj_forward(Tensor input, Tensor weight, Tensor conv_w) {
+    check_bf16(input, "input");
+    check_bf16(weight, "weight");
+    check_bf16(conv_w, "conv_w");
+    TORCH_CHECK(input.dim() == 3, "input must be [B, T, D]");
+    TORCH_CHECK(weight.dim() == 2 && weight.size(1) == input.size(2), "weight dim-1 must equal D");
+    TORCH_CHECK(conv_w.dim() == 2 && conv_w.size(0) == weight.size(0), "conv_w dim-0 must equal D_out");
+    const int64_t B = input.size(0), T = input.size(1), D = input.size(2), Dout = weight.size(0);
+    const c10::DeviceGuard guard(input.device());
+    auto out = at::empty({B, T, Dout}, input.options());
+    GDN_CHECK_STATUS(gdn_proj_conv_silu_hip(bf(input), bf(weight), bf(conv_w), bf_mut(out), B, T, D, Dout,
+                                            conv_w.size(1), stream_of(input)),
+                     "proj");
+    return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "MI355X (gfx950) Gated DeltaNet kernels: torch binding over libgdn_amd.so";
+    m.attr("ABI_VERSION") = gdn_abi_version();
+
+    auto mp = m.def_submodule("prefill", "GDN chunked prefill (chunk 64)");
+    mp.def("prefill", &prefill,
+           "Args: q,k [B,H,T,K] bf16 | v [B,H,T,V] bf16 | A_log [H] fp32 | a,b_logits [B,H,T] bf16 | "
+           "dt_bias float | mask [B,T] fp32 (empty = ones) | state_in [B,H,K,V] fp32 (empty = zeros) | "
+           "scale float (0 = K^-0.5)\nReturns: (out [B,H,T,V] bf16, state_out [B,H,K,V] fp32)",
+           py::arg("q"), py::arg("k"), py::arg("v"), py::arg("A_log"), py::arg("a"), py::arg("dt_bias"),
+           py::arg("b_logits"), py::arg("mask"), py::arg("state_in"), py::arg("scale"));
+    mp.def("prefill_varlen", &prefill_varlen,
+           "Packed varlen prefill: q,k [1,H,Ttot,K] | v [1,H,Ttot,V] | a,b_logits [1,H,Ttot] | cu_seqlens [N+1] | "
+           "state_in [N,H,K,V] or empty.  Returns (out [1,H,Ttot,V] bf16, state_out [N,H,K,V] fp32)",
+           py::arg("q"), py::arg("k"), py::arg("v"), py::arg("A_log"), py::arg("a"), py::arg("dt_bias"),
+           py::arg("b_logits"), py::arg("cu_seqlens"), py::arg("state_in"), py::arg("scale"),
+           py::arg("mask") = py::none(), py::arg("max_seqlen") = 0);
+    // Reference attribute values; H and V are runtime parameters here (any H,
+    // V % 16 == 0), K is 128 and the chunk is 64 as in the reference.
+    mp.attr("H_DIM") = 16;
+    mp.attr("K_DIM") = 128;
+    mp.attr("V_DIM") = 256;
+    mp.attr("C_DIM") = 64;
+
+    auto md = m.def_submodule("decode", "GDN decode step");
+    md.def("forward", &decode_forward, "GDN decode forward (S_out may alias S_in)", py::arg("q"), py::arg("k"),
+           py::arg("v"), py::arg("a"), py::arg("b"), py::arg("A_log"), py::arg("dt_bias"), py::arg("S_in"),
+           py::arg("scale"), py::arg("o_out"), py::arg("S_out"));
+
+    auto mr = m.def_submodule("rmsnorm", "RMSNorm (bf16)");
+    mr.def("forward", &rmsnorm_forward, "RMSNorm forward (bf16, any D % 8 == 0)", py::arg("x"), py::arg("gamma"),
+           py::arg("eps"), py::arg("block_threads"), py::arg("rows_per_block"));
+
+    auto mj = m.def_submodule("proj", "Projection + causal conv + SiLU");
+    mj.def("forward", &proj_forward, "Fused linear projection + causal depthwise conv1d + SiLU (bf16)",
+           py::arg("input"), py::arg("weight"), py::arg("conv_w"));
+}

@@ -1,0 +1,100 @@
+// Shared device helpers and host-side error plumbing for libgdn_amd.so.
+// gfx950 (CDNA4) only: wave64, bf16 MFMA 16x16x32, 160 KiB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/gdn_amd.h"
+
+namespace gdn {
+
+// ---------------------------------------------------------------------------
+// Vector types used as MFMA operands and for 128-bit memory traffic.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(uint16_t x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+__device__ __forceinline__ float bf2f(bf16 x) { return static_cast<float>(x); }
+
+// Round-to-nearest-even float -> bf16 (gfx950 has a native convert).
+__device__ __forceinline__ bf16 f2bf(float x) { return static_cast<bf16>(x); }
+
+__device__ __forceinline__ uint16_t f2bf_bits(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<bf16>(x));
+}
+
+// Unpack 8 bf16 held in a 128-bit word into floats.
+__device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+// softplus(x) = log(1 + e^x), linear above 20 as in the reference
+// (kernels/decode.cu:36-38); log1pf/expf are the ROCm device library's.
+__device__ __forceinline__ float softplus_f(float x) {
+    return x > 20.f ? x : log1pf(expf(x));
+}
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// Cross-lane sums over groups of 8 consecutive lanes, all DPP (no LDS).
+// quad_perm [1,0,3,2] and [2,3,0,1] give the sum over each quad; the
+// half-row mirror (lane i <-> 7-i inside each 8-lane half row) adds the
+// other quad of the group.  Every lane of the group ends with the total.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    return v;
+}
+
+// MFMA 16x16x32 bf16 -> fp32.  Operand layout used throughout (the k order
+// inside a lane is free as long as A and B agree on it):
+//   A (16 x 32): lane l supplies row l%16, eight k values of group l/16
+//   B (32 x 16): lane l supplies column l%16, the same eight k values
+//   C (16 x 16): lane l holds column l%16, rows 4*(l/16) + i, i = 0..3
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8 a, const bf16x8 b, const f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const f32x4 lo, const f32x4 hi) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = f2bf(lo[i]);
+        r[4 + i] = f2bf(hi[i]);
+    }
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
+
+}  // namespace gdn
+
+// ---------------------------------------------------------------------------
+// Host-side helpers shared by the entry points (defined in abi.cpp).
+// ---------------------------------------------------------------------------
+namespace gdn_host {
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* kernel);
+inline bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+}  // namespace gdn_host

@@ -1,0 +1,36 @@
+// Parameter block of the projection + conv + SiLU kernel (proj.hip), shared
+// with the layer-level fused in-projection entry point.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn_proj {
+
+constexpr int kMaxGroups = 5;
+
+// Columns [col0, col0 + width) of P = x W^T go to dst.  head_dim > 0 writes
+// [B, width / head_dim, T, head_dim]; head_dim == 0 writes [B, T, width].
+// conv != 0 applies the causal depthwise conv (weights conv_w rows cw_row0 +
+// column-in-group) and SiLU; conv == 0 stores the current token's P.
+struct ProjGroup {
+    int col0;
+    int width;
+    int head_dim;
+    int conv;
+    int cw_row0;
+    uint16_t* dst;
+};
+
+struct ProjParams {
+    const uint16_t* x;       // [B, T, D]
+    const uint16_t* W;       // [D_out, D]
+    const uint16_t* conv_w;  // [rows, conv_k]
+    int B, T, D, D_out, conv_k;
+    int ngroups;  // groups sorted by col0, groups[0].col0 == 0
+    ProjGroup groups[kMaxGroups];
+};
+
+int launch_proj(const ProjParams& p, hipStream_t stream);
+
+}  // namespace gdn_proj

@@ -1,0 +1,87 @@
+// RMSNorm for bf16 rows of any D % 8 == 0 (D <= 16384).
+//
+// Reference: kernels/rmsnorm.cu:17-103 (one 32-lane warp per row, D = 2048
+// fixed, scalar 2-byte loads) and reference/rmsnorm_ref.py:8-28 for the math:
+//   y = bf16((x * rsqrt(mean(x^2) + eps)) * gamma), all in fp32.
+// Here one wave64 owns a row; each lane moves 16-byte chunks (8 bf16), the
+// row stays in VGPRs between the sum of squares and the scaling, so x is read
+// once and y written once.  Four rows per 256-thread workgroup.
+#include "gdn_common.hpp"
+
+namespace {
+
+using namespace gdn;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+template <int CHUNKS>  // 16-byte chunks per lane
+__global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ gamma,
+                                                          uint16_t* __restrict__ y, int R, int D, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= R) return;
+    const int nch = D >> 3;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * D);
+    u32x4 xv[CHUNKS];
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < CHUNKS; ++u) {
+        const int c = lane + 64 * u;
+        xv[u] = c < nch ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+        float f[8];
+        unpack8(xv[u], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    }
+    const float inv = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+    const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
+    u32x4* yr = reinterpret_cast<u32x4*>(y + static_cast<size_t>(row) * D);
+#pragma unroll
+    for (int u = 0; u < CHUNKS; ++u) {
+        const int c = lane + 64 * u;
+        if (c < nch) {
+            float f[8], gm[8];
+            unpack8(xv[u], f);
+            unpack8(gr[c], gm);
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = f2bf_bits((f[2 * e] * inv) * gm[2 * e]);
+                const uint32_t hi = f2bf_bits((f[2 * e + 1] * inv) * gm[2 * e + 1]);
+                o[e] = lo | (hi << 16);
+            }
+            yr[c] = o;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int gdn_rmsnorm_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, gdn_bf16_t* y, int R, int D,
+                               float eps, void* stream) {
+    using gdn_host::aligned;
+    using gdn_host::fail;
+    if (R < 0 || D <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "rmsnorm: R=%d D=%d", R, D);
+    if (D % 8 != 0 || D > 16384) return fail(GDN_ERR_UNSUPPORTED, "rmsnorm: D=%d must be a multiple of 8, <= 16384", D);
+    if (R == 0) return GDN_OK;
+    if (!x || !gamma || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "rmsnorm: null pointer argument");
+    if (!aligned(x, 16) || !aligned(gamma, 16) || !aligned(y, 16))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "rmsnorm: buffers need 16-byte alignment");
+    const dim3 grid((R + 3) / 4), block(256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int nch = D / 8;
+    if (nch <= 64 * 4)
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<4>, grid, block, 0, s, x, gamma, y, R, D, eps);
+    else if (nch <= 64 * 8)
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<8>, grid, block, 0, s, x, gamma, y, R, D, eps);
+    else if (nch <= 64 * 16)
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<16>, grid, block, 0, s, x, gamma, y, R, D, eps);
+    else
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<32>, grid, block, 0, s, x, gamma, y, R, D, eps);
+    return gdn_host::check_launch("gdn_rmsnorm_kernel");
+}

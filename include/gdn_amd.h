@@ -1,0 +1,134 @@
+/*
+ * gdn_amd.h — C ABI of the MI355X (gfx950) Gated DeltaNet hot-path library
+ * (libgdn_amd.so).
+ *
+ * Plain pointers and sizes only.  All data pointers are DEVICE pointers unless
+ * a parameter says otherwise; every call is asynchronous on `stream` (a
+ * hipStream_t passed as void*, NULL = the null stream) and returns a status
+ * code.  On failure nothing is launched and gdn_last_error() returns a message
+ * for the calling thread.  bf16 tensors are passed as their 16-bit patterns.
+ *
+ * Reference interfaces replaced (paths into diacccc/GDN_18646):
+ *   gdn_decode_hip            <- extern "C" gdn_decode_cuda, kernels/decode.cu:131-162
+ *                                (and gdn_decode_forward, kernels/decode.cu:172-214)
+ *   gdn_prefill_hip           <- gdn_prefill, kernels/prefill_chunked.cu:422-504
+ *   gdn_prefill_varlen_hip    <- no reference counterpart (packed cu_seqlens prefill);
+ *                                semantics = gdn_prefill per sequence
+ *   gdn_rmsnorm_hip           <- rmsnorm_forward_impl / launch_rmsnorm,
+ *                                kernels/rmsnorm.cu:112-131,251-276
+ *   gdn_proj_conv_silu_hip    <- fused_proj_conv_silu, kernels/fused_proj_conv_silu.cu:298-355
+ */
+#ifndef GDN_AMD_H
+#define GDN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t gdn_bf16_t; /* bfloat16 bit pattern */
+
+enum {
+    GDN_OK = 0,
+    GDN_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misaligned buffer */
+    GDN_ERR_UNSUPPORTED = 2,      /* shape outside what the kernels are built for */
+    GDN_ERR_WORKSPACE = 3,        /* workspace missing or smaller than required */
+    GDN_ERR_HIP = 4               /* a HIP runtime call or launch failed */
+};
+
+/* Library version, e.g. 1 for this interface revision. */
+int gdn_abi_version(void);
+
+/* Human-readable text for a status code, and the last error of this thread. */
+const char* gdn_status_string(int status);
+const char* gdn_last_error(void);
+
+/*
+ * Decode: one token per sequence, state updated as
+ *   S <- g S ; r = k^T S ; S <- S + k (beta (v - r))^T ; o = scale q^T S
+ * with g = exp(-exp(A_log[h]) softplus(a + dt_bias[h])), beta = sigmoid(b).
+ *   q, k     [B, H, dk]   bf16        v        [B, H, dv] bf16
+ *   a, b     [B, H]       bf16        A_log, dt_bias [H] fp32
+ *   S_in     [B, H, dk, dv] fp32      o        [B, H, dv] fp32
+ *   S_out    [B, H, dk, dv] fp32 — may be the same buffer as S_in (in place)
+ * Supported: dk == 128, dv % 32 == 0, 32 <= dv <= 1024.  Buffers 16-byte aligned.
+ * Replaces gdn_decode_cuda (kernels/decode.cu:131-162), which took no stream,
+ * returned nothing and silently did nothing for an unsupported dv.
+ */
+int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                   const gdn_bf16_t* a, const gdn_bf16_t* b,
+                   const float* A_log, const float* dt_bias,
+                   const float* S_in, float scale,
+                   float* o, float* S_out,
+                   int B, int H, int dk, int dv, void* stream);
+
+/*
+ * Chunked prefill (chunk size 64) of B equal-length sequences.
+ *   q, k [B, H, T, dk] bf16; v [B, H, T, dv] bf16; a, b_logits [B, H, T] bf16
+ *   A_log [H] fp32; dt_bias scalar; mask [B, T] fp32 or NULL (all ones)
+ *   state_in [B, H, dk, dv] fp32 or NULL (zero state)
+ *   out [B, H, T, dv] bf16; state_out [B, H, dk, dv] fp32
+ * scale == 0 means dk^-0.5.  Any T >= 1.  Supported: dk == 128, dv % 16 == 0,
+ * 16 <= dv <= 512.  Masked tokens decay the state but write nothing, and their
+ * outputs are zero (reference/prefill_ref.py:79-80,130).
+ * workspace: device buffer of at least gdn_prefill_workspace_bytes(B, H, T,
+ * dk, dv) bytes, 256-byte aligned; it holds per-chunk intermediates.
+ * Replaces gdn_prefill (kernels/prefill_chunked.cu:422-504), which required
+ * H == 16, dv == 256 and T % 64 == 0 and allocated its outputs itself.
+ */
+size_t gdn_prefill_workspace_bytes(int B, int H, int T, int dk, int dv);
+
+int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                    const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                    const gdn_bf16_t* b_logits, const float* mask,
+                    const float* state_in, float scale,
+                    gdn_bf16_t* out, float* state_out,
+                    int B, int H, int T, int dk, int dv,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Packed variable-length prefill: num_seqs sequences concatenated along T.
+ *   q, k [H, T_total, dk]; v [H, T_total, dv]; a, b_logits [H, T_total]
+ *   cu_seqlens: DEVICE int32 [num_seqs + 1], non-decreasing, cu[0] = 0,
+ *               cu[num_seqs] = T_total
+ *   max_seqlen: upper bound on any sequence length (<= 0: T_total is used)
+ *   mask [T_total] fp32 or NULL; state_in [num_seqs, H, dk, dv] or NULL
+ *   out [H, T_total, dv] bf16; state_out [num_seqs, H, dk, dv] fp32
+ * Each sequence is an independent prefill (state does not cross sequences).
+ */
+size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int dk, int dv);
+
+int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                           const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                           const gdn_bf16_t* b_logits, const float* mask,
+                           const int32_t* cu_seqlens, int num_seqs, int max_seqlen,
+                           const float* state_in, float scale,
+                           gdn_bf16_t* out, float* state_out,
+                           int H, int T_total, int dk, int dv,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * RMSNorm: y[r, :] = bf16(x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * gamma).
+ *   x, y [R, D] bf16 (may not alias); gamma [D] bf16.  D % 8 == 0, D <= 16384.
+ */
+int gdn_rmsnorm_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, gdn_bf16_t* y,
+                    int R, int D, float eps, void* stream);
+
+/*
+ * Projection + causal depthwise conv (taps conv_k) + SiLU, fp32 accumulation:
+ *   out[b, t, c] = bf16(SiLU(sum_j conv_w[c, j] * P[b, t - conv_k + 1 + j, c]))
+ *   P = x W^T with P[b, t<0, :] = 0.
+ *   x [B, T, D] bf16; W [D_out, D] bf16; conv_w [D_out, conv_k] bf16;
+ *   out [B, T, D_out] bf16.  D % 64 == 0, D_out % 16 == 0, conv_k in 1..4.
+ */
+int gdn_proj_conv_silu_hip(const gdn_bf16_t* x, const gdn_bf16_t* W,
+                           const gdn_bf16_t* conv_w, gdn_bf16_t* out,
+                           int B, int T, int D, int D_out, int conv_k, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_AMD_H */
