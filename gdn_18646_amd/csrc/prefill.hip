@@ -258,170 +258,292 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
 // ---------------------------------------------------------------------------
 // Kernel 2
 // ---------------------------------------------------------------------------
-template <int NT>
-__global__ __launch_bounds__(64) void gdn_prefill_state_kernel(PrefillParams p, int nvt, int nheads,
-                                                               int xcd_map) {
-    // blockIdx -> (head, column tile).  With xcd_map the column tiles of one
-    // head land on the same XCD (workgroups are dealt to the 8 XCDs round
-    // robin), so the per-chunk operands they all read share one L2.
+// Per-chunk operands staged in LDS (one buffer; the kernel double-buffers).
+// Every block is a run of 1 KiB "fragments": 64 lanes x 16 bytes, lane l's
+// 16 bytes at offset 16 l, i.e. exactly one MFMA operand register quad.
+constexpr int kFragB = 1024;
+constexpr int kOffK = 0;                   // 16 fragments (mt, s): K rows 16mt+m, k 32s+8g..+7
+constexpr int kOffQ = kOffK + 16 * kFragB;  // 16 fragments, same order for Q
+constexpr int kOffT = kOffQ + 16 * kFragB;  // 8 fragments of Tp
+constexpr int kOffA = kOffT + 8 * kFragB;   // 8 fragments of Aq
+constexpr int kOffKt = kOffA + 8 * kFragB;  // 16 fragments of Kt
+constexpr int kOffG = kOffKt + 16 * kFragB; // gates: gamma[64], m scale gamma[64] (1 KiB slot)
+constexpr int kOffV = kOffG + kFragB;       // per wave: V[64][16] bf16 (2 KiB)
+__host__ __device__ constexpr int state_buf_bytes(int nw) { return kOffV + nw * 2 * kFragB; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+
+// 16 bytes per lane from g (per-lane address) to lds_base + 16 lane; lds_base
+// must be uniform over the wave.  Asynchronous: completion is vmcnt.  Issued
+// as inline asm so the compiler's wait-count pass does not drain the copy
+// before unrelated LDS reads of the other buffer (it cannot prove they do not
+// alias); the kernel orders copies with its own vmcnt waits and barriers.
+// M0 is otherwise unused on gfx950 (LDS instructions do not read it), so the
+// clobber is safe here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, lds_u8* lds_base) {
+    const uint32_t m0v = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0v), "v"(g)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Workgroup barrier for LDS producer/consumer hand-off: LDS writes of this
+// wave complete, then all waves meet.  (Async copies are covered by the
+// vmcnt wait that precedes it.)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt immediates (gfx9 layout: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+__device__ __forceinline__ void wait_vm16() { __builtin_amdgcn_s_waitcnt(0x4F70); }  // vmcnt(16)
+// A full chunk issues exactly this many output stores per wave after the
+// next chunk's copies; vector memory ops complete in issue order, so waiting
+// for vmcnt <= kStoresPerChunk means the copies have landed.
+constexpr int kStoresPerChunk = 16;
+
+// Per-lane byte offsets of the staging copies, fixed for the whole kernel.
+struct StageLane {
+    uint32_t kq;  // K/Q fragment: row (lane & 15), k offset 8 (lane >> 4)
+    uint32_t fr;  // workspace fragment: 16 lane
+    uint32_t g;   // gate block: 16 (lane & 31)
+    uint32_t v;   // V tile: row (lane >> 1), 8 columns (lane & 1)
+};
+
+// Stage chunk operands into `buf`.  Full chunks use uniform bases plus the
+// lane offsets; the last, partial chunk clamps rows to the sequence (so no
+// load leaves the tensors) and its padded rows are zeroed after arrival.
+template <int NW>
+__device__ __forceinline__ void stage_chunk(const PrefillParams& p, lds_u8* buf, size_t row_base, int nvalid,
+                                            size_t wc, int wave, int lane, int col0_wave, const StageLane& L) {
+    const unsigned char* tb = reinterpret_cast<const unsigned char*>(p.wsT + wc * 8 * 64);
+    const unsigned char* ab = reinterpret_cast<const unsigned char*>(p.wsA + wc * 8 * 64);
+    const unsigned char* ktb = reinterpret_cast<const unsigned char*>(p.wsK + wc * 16 * 64);
+    const unsigned char* gb = reinterpret_cast<const unsigned char*>(p.wsG + wc * 128);
+    if (nvalid == kC) {
+        const unsigned char* kb = reinterpret_cast<const unsigned char*>(p.k + row_base * kDK);
+        const unsigned char* qb = reinterpret_cast<const unsigned char*>(p.q + row_base * kDK);
+#pragma unroll
+        for (int f = 0; f < 16; ++f) {
+            const uint32_t o = L.kq + (f >> 2) * 16 * kDK * 2 + (f & 3) * 64;
+            if (f % NW == wave) dma16(kb + o, buf + kOffK + f * kFragB);
+            if ((f + 16) % NW == wave) dma16(qb + o, buf + kOffQ + f * kFragB);
+        }
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+            dma16(reinterpret_cast<const unsigned char*>(p.v + (row_base + 32 * it) * p.dv) + L.v,
+                  buf + kOffV + wave * 2 * kFragB + it * kFragB);
+    } else {
+        const int m = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int f = 0; f < 16; ++f) {
+            const int row = min(16 * (f >> 2) + m, nvalid - 1);
+            const size_t e = (row_base + row) * kDK + 32 * (f & 3) + 8 * g;
+            if (f % NW == wave) dma16(p.k + e, buf + kOffK + f * kFragB);
+            if ((f + 16) % NW == wave) dma16(p.q + e, buf + kOffQ + f * kFragB);
+        }
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int row = min(32 * it + (lane >> 1), nvalid - 1);
+            dma16(p.v + (row_base + row) * p.dv + col0_wave + 8 * (lane & 1), buf + kOffV + wave * 2 * kFragB + it * kFragB);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+        if ((f + 32) % NW == wave) dma16(tb + f * kFragB + L.fr, buf + kOffT + f * kFragB);
+        if ((f + 40) % NW == wave) dma16(ab + f * kFragB + L.fr, buf + kOffA + f * kFragB);
+    }
+#pragma unroll
+    for (int f = 0; f < 16; ++f)
+        if ((f + 48) % NW == wave) dma16(ktb + f * kFragB + L.fr, buf + kOffKt + f * kFragB);
+    if (64 % NW == wave) dma16(gb + L.g, buf + kOffG);
+}
+
+// Zero the rows >= nvalid of the staged K, Q and V (partial chunk only).
+template <int NW>
+__device__ __forceinline__ void zero_pad_rows(lds_u8* buf, int nvalid, int wave, int lane) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    if (16 * 0 + (lane & 15) >= 0) {
+#pragma unroll
+        for (int f = 0; f < 32; ++f)
+            if (f % NW == wave && 16 * ((f & 15) >> 2) + (lane & 15) >= nvalid)
+                *reinterpret_cast<lds_u32x4*>(buf + kOffK + f * kFragB + 16 * lane) = z;  // K then Q (contiguous)
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+        if (32 * it + (lane >> 1) >= nvalid)
+            *reinterpret_cast<lds_u32x4*>(buf + kOffV + wave * 2 * kFragB + it * kFragB + 16 * lane) = z;
+}
+
+__device__ __forceinline__ bf16x8 frag(const lds_u8* buf, int off, int lane) {
+    return *reinterpret_cast<const lds_bf16x8*>(buf + off + 16 * lane);
+}
+
+// One chunk of the state recurrence for a 128 x 16 column tile, operands in LDS.
+// `ob` points at out[row_base][0] (uniform); `oo` = this lane's column offset.
+__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8], uint16_t* ob, int dv,
+                                            int nvalid, int wave, int lane, int col) {
+    const int n = lane & 15, g = lane >> 4;
+    const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + kOffG);
+    const lds_u16* Vs = reinterpret_cast<const lds_u16*>(buf + kOffV + wave * 2 * kFragB);
+
+    // (a) X = K S, P = Q S.
+    f32x4 X[4], P[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) X[mt] = P[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const bf16x8 Bs = pack8(S[2 * s], S[2 * s + 1]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            X[mt] = mfma16x16x32(frag(buf, kOffK + (4 * mt + s) * kFragB, lane), Bs, X[mt]);
+            P[mt] = mfma16x16x32(frag(buf, kOffQ + (4 * mt + s) * kFragB, lane), Bs, P[mt]);
+        }
+    }
+    // (b) Y = V - gamma o X (in place in X).
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const f32x4 gam = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X[mt][i] = bf2f(Vs[(16 * mt + 4 * g + i) * 16 + n]) - gam[i] * X[mt][i];
+    }
+    // (c) dV = Tp Y.
+    f32x4 D[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) D[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const bf16x8 BY = pack8(X[2 * s], X[2 * s + 1]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) D[mt] = mfma16x16x32(frag(buf, kOffT + (2 * mt + s) * kFragB, lane), BY, D[mt]);
+    }
+    const bf16x8 BD0 = pack8(D[0], D[1]);
+    const bf16x8 BD1 = pack8(D[2], D[3]);
+    // (e) S <- gamma_C S + Kt dV  (issued before (d): it is the recurrence's critical path).
+    const float gC = G[kC - 1];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        S[r] *= gC;
+        S[r] = mfma16x16x32(frag(buf, kOffKt + (2 * r) * kFragB, lane), BD0, S[r]);
+        S[r] = mfma16x16x32(frag(buf, kOffKt + (2 * r + 1) * kFragB, lane), BD1, S[r]);
+    }
+    // (d) O = (m scale gamma) o P + Aq dV -> bf16.
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const f32x4 co = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
+        f32x4 O = co * P[mt];
+        O = mfma16x16x32(frag(buf, kOffA + (2 * mt) * kFragB, lane), BD0, O);
+        if (mt >= 2) O = mfma16x16x32(frag(buf, kOffA + (2 * mt + 1) * kFragB, lane), BD1, O);
+        if (nvalid == kC) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ob[(16 * mt + 4 * g + i) * dv + col] = f2bf_bits(O[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * mt + 4 * g + i;
+                if (row < nvalid) ob[row * dv + col] = f2bf_bits(O[i]);
+            }
+        }
+    }
+}
+
+// One workgroup = NW waves = NW column tiles of 16 of one (sequence, head).
+// The chunk operands are shared by the waves and double-buffered in LDS: the
+// copies for chunk c+1 are in flight while chunk c is computed.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParams p, int nvg, int nheads,
+                                                                    int xcd_map) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][state_buf_bytes(NW)];
+    lds_u8* const buf0 = (lds_u8*)&smem[0][0];
+    lds_u8* const buf1 = (lds_u8*)&smem[1][0];
+
+    // blockIdx -> (head, column group).  With xcd_map the column groups of a
+    // head land on one XCD (workgroups are dealt to the 8 XCDs round robin),
+    // so the operands they all read share that XCD's L2.
     const int wg = blockIdx.x;
-    int head, vt;
+    int head, vg;
     if (xcd_map) {
         const int xcd = wg & 7, j = wg >> 3;
-        vt = j % nvt;
-        head = (j / nvt) * 8 + xcd;
+        vg = j % nvg;
+        head = (j / nvg) * 8 + xcd;
     } else {
-        vt = wg % nvt;
-        head = wg / nvt;
+        vg = wg % nvg;
+        head = wg / nvg;
     }
-    if (head >= nheads) return;
+    if (head >= nheads) return;  // uniform over the workgroup
     const int sidx = head / p.H;
     const int h = head % p.H;
     const SeqInfo sq = seq_info(p, sidx);
-    const int lane = threadIdx.x;
-    const int n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
     const int dv = p.dv;
-    const int colbase = vt * 16 * NT + n;
+    const int col0_wave = (vg * NW + wave) * 16;
+    const int col = col0_wave + (lane & 15);
+    const StageLane L = {static_cast<uint32_t>((lane & 15) * kDK * 2 + (lane >> 4) * 16),
+                         static_cast<uint32_t>(16 * lane), static_cast<uint32_t>(16 * (lane & 31)),
+                         static_cast<uint32_t>((lane >> 1) * dv * 2 + (lane & 1) * 16 + col0_wave * 2)};
 
-    // State tile: S[r][nt][i] = S[rho(r, g, i)][colbase + 16 nt].
-    f32x4 S[8][NT];
-    {
-        const float* sin = p.state_in ? p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv : nullptr;
+    // State tile: S[r][i] = S[rho(r, g, i)][col].
+    f32x4 S[8];
+    if (p.state_in) {
+        const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+            for (int i = 0; i < 4; ++i) S[r][i] = sin[rho_row(r, g, i) * dv + col];
+    } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    S[r][nt][i] = sin ? sin[static_cast<size_t>(rho_row(r, g, i)) * dv + colbase + 16 * nt] : 0.f;
+        for (int r = 0; r < 8; ++r) S[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     const int nchunks = (sq.len + kC - 1) / kC;
     const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
-    for (int c = 0; c < nchunks; ++c) {
-        const int nvalid = min(kC, sq.len - c * kC);
-        const size_t row_base = head_row0 + static_cast<size_t>(c) * kC;
-        const size_t wc = static_cast<size_t>(sq.slot0 + c) * p.H + h;
-        const float* G = p.wsG + wc * 128;
-
-        // (a) X = K S and P = Q S; B operand = bf16 of the state accumulators.
-        f32x4 X[4][NT], P[4][NT];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                X[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            bf16x8 Bs[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const int row = 16 * mt + n;
-                u32x4 kw = {0u, 0u, 0u, 0u}, qw = {0u, 0u, 0u, 0u};
-                if (row < nvalid) {
-                    kw = *reinterpret_cast<const u32x4*>(p.k + (row_base + row) * kDK + 32 * s + 8 * g);
-                    qw = *reinterpret_cast<const u32x4*>(p.q + (row_base + row) * kDK + 32 * s + 8 * g);
-                }
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    X[mt][nt] = mfma16x16x32(as_bf16x8(kw), Bs[nt], X[mt][nt]);
-                    P[mt][nt] = mfma16x16x32(as_bf16x8(qw), Bs[nt], P[mt][nt]);
-                }
-            }
+    auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
+    auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
+    auto wcof = [&](int c) { return static_cast<size_t>(sq.slot0 + c) * p.H + h; };
+    auto step = [&](int c, lds_u8* cur, lds_u8* nxt) {
+        // Chunk c's copies were issued before chunk c-1's output stores.
+        if (c == 0)
+            wait_vm0();
+        else
+            wait_vm16();
+        lds_barrier();  // chunk c staged by every wave; nobody still reads `nxt`
+        if (c + 1 < nchunks) stage_chunk<NW>(p, nxt, rows(c + 1), nval(c + 1), wcof(c + 1), wave, lane, col0_wave, L);
+        const int nv = nval(c);
+        if (nv < kC) {
+            zero_pad_rows<NW>(cur, nv, wave, lane);
+            lds_barrier();
         }
+        state_chunk(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col);
+    };
 
-        // (b) Y = V - gamma o X, in the accumulator layout (reuses X).
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const f32x4 gam = *reinterpret_cast<const f32x4*>(G + 16 * mt + 4 * g);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 16 * mt + 4 * g + i;
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const float vv = row < nvalid ? bf2f(p.v[(row_base + row) * dv + colbase + 16 * nt]) : 0.f;
-                    X[mt][nt][i] = vv - gam[i] * X[mt][nt][i];
-                }
-            }
-        }
-
-        // (c) dV = Tp Y.
-        f32x4 D[4][NT];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            bf16x8 BY[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) BY[nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const bf16x8 aT = as_bf16x8(p.wsT[(wc * 8 + mt * 2 + s) * 64 + lane]);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) D[mt][nt] = mfma16x16x32(aT, BY[nt], D[mt][nt]);
-            }
-        }
-        bf16x8 BD[2][NT];
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) BD[s][nt] = pack8(D[2 * s][nt], D[2 * s + 1][nt]);
-
-        // (d) O = (m scale gamma) o P + Aq dV  -> bf16 out.
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const f32x4 co = *reinterpret_cast<const f32x4*>(G + 64 + 16 * mt + 4 * g);
-            f32x4 O[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) O[nt] = co * P[mt][nt];
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                if (s == 1 && mt < 2) continue;  // columns 32..63 are above the diagonal
-                const bf16x8 aA = as_bf16x8(p.wsA[(wc * 8 + mt * 2 + s) * 64 + lane]);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) O[nt] = mfma16x16x32(aA, BD[s][nt], O[nt]);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 16 * mt + 4 * g + i;
-                if (row < nvalid) {
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        p.out[(row_base + row) * dv + colbase + 16 * nt] = f2bf_bits(O[nt][i]);
-                }
-            }
-        }
-
-        // (e) S <- gamma_C S + Kt dV.
-        const float gC = G[kC - 1];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) S[r][nt] *= gC;
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const bf16x8 aK = as_bf16x8(p.wsK[(wc * 16 + r * 2 + s) * 64 + lane]);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) S[r][nt] = mfma16x16x32(aK, BD[s][nt], S[r][nt]);
-            }
-        }
+    if (nchunks > 0) stage_chunk<NW>(p, buf0, rows(0), nval(0), wcof(0), wave, lane, col0_wave, L);
+    for (int c = 0; c < nchunks; c += 2) {
+        step(c, buf0, buf1);
+        if (c + 1 < nchunks) step(c + 1, buf1, buf0);
     }
 
     float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
     for (int r = 0; r < 8; ++r)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                so[static_cast<size_t>(rho_row(r, g, i)) * dv + colbase + 16 * nt] = S[r][nt][i];
+        for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col] = S[r][i];
+}
+
+// ---------------------------------------------------------------------------
+// Zero fill used for the T == 0 state (a kernel rather than a memset node, so
+// the call stays safe to capture in a HIP graph).
+__global__ void gdn_fill_zero_kernel(float* __restrict__ p, size_t n) {
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        p[i] = 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -458,8 +580,9 @@ int check_common(const char* who, int H, int dk, int dv) {
     return GDN_OK;
 }
 
+// phases: bit 0 = chunk-parallel intra kernel, bit 1 = sequential state kernel.
 int launch(PrefillParams& p, int nseq, int nchunk_grid, void* workspace, size_t ws_bytes,
-           long long slots, hipStream_t stream) {
+           long long slots, hipStream_t stream, int phases) {
     using gdn_host::fail;
     const WsLayout L = ws_layout(slots, p.H);
     if (!workspace || ws_bytes < L.total)
@@ -472,24 +595,29 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, void* workspace, size_t 
     p.wsK = reinterpret_cast<u32x4*>(ws + L.offK);
     p.wsG = reinterpret_cast<float*>(ws + L.offG);
 
-    if (nchunk_grid > 0) {
+    if ((phases & 1) && nchunk_grid > 0) {
         hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(nchunk_grid, p.H, nseq), dim3(256), 0, stream, p);
         const int st = gdn_host::check_launch("gdn_prefill_intra_kernel");
         if (st != GDN_OK) return st;
     }
+    if (!(phases & 2)) return GDN_OK;
     const int nheads = nseq * p.H;
-    const long long waves16 = static_cast<long long>(nheads) * (p.dv / 16);
-    const int NT = (waves16 >= 4096 && p.dv % 32 == 0) ? 2 : 1;
-    const int nvt = p.dv / (16 * NT);
+    const long long waves = static_cast<long long>(nheads) * (p.dv / 16);
+    // Waves per workgroup: one while the grid is smaller than the CU count
+    // (latency-bound, each wave gets a CU), more to share LDS staging after.
+    int NW = waves <= 256 ? 1 : (waves <= 512 ? 2 : 4);
+    while ((p.dv / 16) % NW) NW >>= 1;
+    const int nvg = p.dv / (16 * NW);
     const int xcd_map = (nheads % 8 == 0) ? 1 : 0;
-    const long long nwg = static_cast<long long>(nheads) * nvt;
+    const long long nwg = static_cast<long long>(nheads) * nvg;
     if (nwg > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-    if (NT == 2)
-        hipLaunchKernelGGL(gdn_prefill_state_kernel<2>, dim3(static_cast<unsigned>(nwg)), dim3(64), 0, stream, p,
-                           nvt, nheads, xcd_map);
+    const dim3 grid(static_cast<unsigned>(nwg));
+    if (NW == 4)
+        hipLaunchKernelGGL(gdn_prefill_state_kernel<4>, grid, dim3(256), 0, stream, p, nvg, nheads, xcd_map);
+    else if (NW == 2)
+        hipLaunchKernelGGL(gdn_prefill_state_kernel<2>, grid, dim3(128), 0, stream, p, nvg, nheads, xcd_map);
     else
-        hipLaunchKernelGGL(gdn_prefill_state_kernel<1>, dim3(static_cast<unsigned>(nwg)), dim3(64), 0, stream, p,
-                           nvt, nheads, xcd_map);
+        hipLaunchKernelGGL(gdn_prefill_state_kernel<1>, grid, dim3(64), 0, stream, p, nvg, nheads, xcd_map);
     return gdn_host::check_launch("gdn_prefill_state_kernel");
 }
 
@@ -513,10 +641,14 @@ size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int 
     return ws_layout(slots, H).total;
 }
 
-int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
-                    const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
-                    const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H,
-                    int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int prefill_batch(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                  const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                  const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H, int T,
+                  int dk, int dv, void* workspace, size_t workspace_bytes, void* stream, int phases) {
     using gdn_host::aligned;
     using gdn_host::fail;
     int st = check_common("prefill", H, dk, dv);
@@ -551,17 +683,46 @@ int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* 
     const long long slots = static_cast<long long>(B) * p.chunks_per_seq;
     if (slots == 0) {
         // T == 0: the state passes through unchanged.
+        if (!(phases & 2)) return GDN_OK;
         if (state_in)
             return hipMemcpyAsync(state_out, state_in, static_cast<size_t>(B) * H * dk * dv * 4,
                                   hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)) == hipSuccess
                        ? GDN_OK
                        : fail(GDN_ERR_HIP, "prefill: state copy failed");
-        return hipMemsetAsync(state_out, 0, static_cast<size_t>(B) * H * dk * dv * 4,
-                              static_cast<hipStream_t>(stream)) == hipSuccess
-                   ? GDN_OK
-                   : fail(GDN_ERR_HIP, "prefill: state clear failed");
+        hipLaunchKernelGGL(gdn_fill_zero_kernel, dim3(1024), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           state_out, static_cast<size_t>(B) * H * dk * dv);
+        return gdn_host::check_launch("gdn_fill_zero_kernel");
     }
-    return launch(p, B, p.chunks_per_seq, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream));
+    return launch(p, B, p.chunks_per_seq, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream),
+                  phases);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                    const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                    const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H,
+                    int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
+    return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
+                         dv, workspace, workspace_bytes, stream, 3);
+}
+
+int gdn_prefill_intra_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                          const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                          const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H,
+                          int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
+    return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
+                         dv, workspace, workspace_bytes, stream, 1);
+}
+
+int gdn_prefill_state_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                          const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                          const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H,
+                          int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
+    return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
+                         dv, workspace, workspace_bytes, stream, 2);
 }
 
 int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
@@ -604,7 +765,7 @@ int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_b
     const int maxlen = (max_seqlen > 0 && max_seqlen < T_total) ? max_seqlen : T_total;
     const int nchunk_grid = (maxlen + kC - 1) / kC;
     const long long slots = static_cast<long long>(T_total) / kC + num_seqs + 1;
-    return launch(p, num_seqs, nchunk_grid, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream));
+    return launch(p, num_seqs, nchunk_grid, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream), 3);
 }
 
 }  // extern "C"

@@ -89,6 +89,32 @@ int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* 
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The two phases of gdn_prefill_hip, same arguments, for callers that overlap
+ * them with other work (and for per-phase timing):
+ *   intra — every chunk in parallel: reads q, k, a, b_logits, mask, A_log,
+ *           dt_bias, scale; fills `workspace` (out/state pointers unused);
+ *   state — chunks in order per (sequence, head): reads the workspace, q, k,
+ *           v, state_in; writes out and state_out.
+ * gdn_prefill_hip is intra followed by state on the same stream.  No
+ * reference counterpart (the reference runs one fused kernel).
+ */
+int gdn_prefill_intra_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                          const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                          const gdn_bf16_t* b_logits, const float* mask,
+                          const float* state_in, float scale,
+                          gdn_bf16_t* out, float* state_out,
+                          int B, int H, int T, int dk, int dv,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+int gdn_prefill_state_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                          const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                          const gdn_bf16_t* b_logits, const float* mask,
+                          const float* state_in, float scale,
+                          gdn_bf16_t* out, float* state_out,
+                          int B, int H, int T, int dk, int dv,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Packed variable-length prefill: num_seqs sequences concatenated along T.
  *   q, k [H, T_total, dk]; v [H, T_total, dv]; a, b_logits [H, T_total]
  *   cu_seqlens: DEVICE int32 [num_seqs + 1], non-decreasing, cu[0] = 0,
