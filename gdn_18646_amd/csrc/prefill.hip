@@ -386,12 +386,43 @@ __device__ __forceinline__ bf16x8 frag(const lds_u8* buf, int off, int lane) {
 }
 
 // One chunk of the state recurrence for a 128 x 16 column tile, operands in LDS.
-// `ob` points at out[row_base][0] (uniform); `oo` = this lane's column offset.
-__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8], uint16_t* ob, int dv,
-                                            int nvalid, int wave, int lane, int col) {
+// `ob` points at out[row_base][0] (uniform).  All operand fragments are read
+// from LDS up front (none depends on the state), so the MFMA chain that does
+// depend on it never waits on LDS in between.
+__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8], uint16_t* ob, int dv, int nvalid,
+                                            int wave, int lane, int col) {
     const int n = lane & 15, g = lane >> 4;
     const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + kOffG);
     const lds_u16* Vs = reinterpret_cast<const lds_u16*>(buf + kOffV + wave * 2 * kFragB);
+
+    bf16x8 kf[16], qf[16], tf[8], af[6], ktf[16];
+#pragma unroll
+    for (int f = 0; f < 16; ++f) {
+        kf[f] = frag(buf, kOffK + f * kFragB, lane);
+        qf[f] = frag(buf, kOffQ + f * kFragB, lane);
+    }
+#pragma unroll
+    for (int f = 0; f < 8; ++f) tf[f] = frag(buf, kOffT + f * kFragB, lane);
+    af[0] = frag(buf, kOffA + 0 * kFragB, lane);
+    af[1] = frag(buf, kOffA + 2 * kFragB, lane);
+    af[2] = frag(buf, kOffA + 4 * kFragB, lane);
+    af[3] = frag(buf, kOffA + 5 * kFragB, lane);
+    af[4] = frag(buf, kOffA + 6 * kFragB, lane);
+    af[5] = frag(buf, kOffA + 7 * kFragB, lane);
+#pragma unroll
+    for (int f = 0; f < 16; ++f) ktf[f] = frag(buf, kOffKt + f * kFragB, lane);
+    float vv[16];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[4 * mt + i] = bf2f(Vs[(16 * mt + 4 * g + i) * 16 + n]);
+    f32x4 gam[4], co[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
+        co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
+    }
+    const float gC = G[kC - 1];
 
     // (a) X = K S, P = Q S.
     f32x4 X[4], P[4];
@@ -402,17 +433,15 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8], ui
         const bf16x8 Bs = pack8(S[2 * s], S[2 * s + 1]);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            X[mt] = mfma16x16x32(frag(buf, kOffK + (4 * mt + s) * kFragB, lane), Bs, X[mt]);
-            P[mt] = mfma16x16x32(frag(buf, kOffQ + (4 * mt + s) * kFragB, lane), Bs, P[mt]);
+            X[mt] = mfma16x16x32(kf[4 * mt + s], Bs, X[mt]);
+            P[mt] = mfma16x16x32(qf[4 * mt + s], Bs, P[mt]);
         }
     }
     // (b) Y = V - gamma o X (in place in X).
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const f32x4 gam = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) X[mt][i] = bf2f(Vs[(16 * mt + 4 * g + i) * 16 + n]) - gam[i] * X[mt][i];
-    }
+        for (int i = 0; i < 4; ++i) X[mt][i] = vv[4 * mt + i] - gam[mt][i] * X[mt][i];
     // (c) dV = Tp Y.
     f32x4 D[4];
 #pragma unroll
@@ -421,33 +450,33 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8], ui
     for (int s = 0; s < 2; ++s) {
         const bf16x8 BY = pack8(X[2 * s], X[2 * s + 1]);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) D[mt] = mfma16x16x32(frag(buf, kOffT + (2 * mt + s) * kFragB, lane), BY, D[mt]);
+        for (int mt = 0; mt < 4; ++mt) D[mt] = mfma16x16x32(tf[2 * mt + s], BY, D[mt]);
     }
     const bf16x8 BD0 = pack8(D[0], D[1]);
     const bf16x8 BD1 = pack8(D[2], D[3]);
     // (e) S <- gamma_C S + Kt dV  (issued before (d): it is the recurrence's critical path).
-    const float gC = G[kC - 1];
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         S[r] *= gC;
-        S[r] = mfma16x16x32(frag(buf, kOffKt + (2 * r) * kFragB, lane), BD0, S[r]);
-        S[r] = mfma16x16x32(frag(buf, kOffKt + (2 * r + 1) * kFragB, lane), BD1, S[r]);
+        S[r] = mfma16x16x32(ktf[2 * r], BD0, S[r]);
+        S[r] = mfma16x16x32(ktf[2 * r + 1], BD1, S[r]);
     }
     // (d) O = (m scale gamma) o P + Aq dV -> bf16.
+    f32x4 O[4];
+    O[0] = mfma16x16x32(af[0], BD0, co[0] * P[0]);
+    O[1] = mfma16x16x32(af[1], BD0, co[1] * P[1]);
+    O[2] = mfma16x16x32(af[3], BD1, mfma16x16x32(af[2], BD0, co[2] * P[2]));
+    O[3] = mfma16x16x32(af[5], BD1, mfma16x16x32(af[4], BD0, co[3] * P[3]));
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-        const f32x4 co = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
-        f32x4 O = co * P[mt];
-        O = mfma16x16x32(frag(buf, kOffA + (2 * mt) * kFragB, lane), BD0, O);
-        if (mt >= 2) O = mfma16x16x32(frag(buf, kOffA + (2 * mt + 1) * kFragB, lane), BD1, O);
         if (nvalid == kC) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ob[(16 * mt + 4 * g + i) * dv + col] = f2bf_bits(O[i]);
+            for (int i = 0; i < 4; ++i) ob[(16 * mt + 4 * g + i) * dv + col] = f2bf_bits(O[mt][i]);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = 16 * mt + 4 * g + i;
-                if (row < nvalid) ob[row * dv + col] = f2bf_bits(O[i]);
+                if (row < nvalid) ob[row * dv + col] = f2bf_bits(O[mt][i]);
             }
         }
     }
