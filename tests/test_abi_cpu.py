@@ -1,0 +1,108 @@
+"""CPU checks of the drop-in boundary: the C ABI library and the torch binding.
+
+No kernel is launched: the library loads, exports every entry point that
+include/gdn_amd.h declares, its pure-host functions answer, and argument
+validation rejects bad calls before any HIP call is made.
+"""
+
+import os
+import re
+
+import pytest
+import torch
+
+from gdn_18646_amd import abi, compile_kernels
+from gdn_18646_amd.abi import GdnError
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    src = open(os.path.join(ROOT, "include", "gdn_amd.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = abi.load()
+    names = _declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/gdn_amd.h but not exported"
+    assert set(names) == set(abi.SIGNATURES), "abi.SIGNATURES out of sync with the header"
+
+
+def test_host_functions():
+    lib = abi.load()
+    assert lib.gdn_abi_version() == 1
+    assert lib.gdn_status_string(0) == b"ok"
+    assert lib.gdn_status_string(3) == b"workspace too small"
+    # 32.5 KiB per (chunk, head) plus alignment; the metric shape has 128 chunks x 16 heads
+    b = lib.gdn_prefill_workspace_bytes(1, 16, 8192, 128, 128)
+    assert 2048 * (8 + 8 + 16) * 1024 + 2048 * 512 <= b < 2048 * 33 * 1024 + 4096
+    assert lib.gdn_prefill_workspace_bytes(1, 16, 0, 128, 128) == 0
+    assert lib.gdn_prefill_varlen_workspace_bytes(3, 2, 130, 128, 64) >= (130 // 64 + 3) * 2 * 32 * 1024
+
+
+FAKE = 4096  # non-null, 16-byte aligned; validation fails before it is ever dereferenced
+
+
+def test_decode_validation_errors():
+    with pytest.raises(GdnError, match="UNSUPPORTED.*dk=64"):
+        abi.call("gdn_decode_hip", *([FAKE] * 8), 0.1, FAKE, FAKE, 2, 2, 64, 128, None)
+    with pytest.raises(GdnError, match="UNSUPPORTED.*dv=48"):
+        abi.call("gdn_decode_hip", *([FAKE] * 8), 0.1, FAKE, FAKE, 2, 2, 128, 48, None)
+    with pytest.raises(GdnError, match="INVALID_ARGUMENT.*null"):
+        abi.call("gdn_decode_hip", None, *([FAKE] * 7), 0.1, FAKE, FAKE, 2, 2, 128, 128, None)
+    with pytest.raises(GdnError, match="alignment"):
+        abi.call("gdn_decode_hip", FAKE + 2, *([FAKE] * 7), 0.1, FAKE, FAKE, 2, 2, 128, 128, None)
+    # B == 0 is a valid no-op
+    abi.call("gdn_decode_hip", *([None] * 8), 0.1, None, None, 0, 2, 128, 128, None)
+
+
+def test_prefill_validation_errors():
+    args = [FAKE] * 5 + [0.0, FAKE, None, None, 0.0, FAKE, FAKE]
+    with pytest.raises(GdnError, match="UNSUPPORTED.*dv=40"):
+        abi.call("gdn_prefill_hip", *args, 1, 2, 64, 128, 40, FAKE, 1 << 20, None)
+    with pytest.raises(GdnError, match="UNSUPPORTED.*dk=256"):
+        abi.call("gdn_prefill_hip", *args, 1, 2, 64, 256, 128, FAKE, 1 << 20, None)
+    with pytest.raises(GdnError, match="WORKSPACE"):
+        abi.call("gdn_prefill_hip", *args, 1, 2, 64, 128, 128, FAKE, 16, None)
+    with pytest.raises(GdnError, match="WORKSPACE"):
+        abi.call("gdn_prefill_hip", *args, 1, 2, 64, 128, 128, None, 1 << 30, None)
+    with pytest.raises(GdnError, match="INVALID_ARGUMENT"):
+        abi.call("gdn_prefill_varlen_hip", *([FAKE] * 5), 0.0, FAKE, None, None, 3, 0, None, 0.0, FAKE, FAKE,
+                 2, 64, 128, 128, FAKE, 1 << 30, None)
+
+
+def test_support_validation_errors():
+    with pytest.raises(GdnError, match="multiple of 8"):
+        abi.call("gdn_rmsnorm_hip", FAKE, FAKE, FAKE, 4, 100, 1e-6, None)
+    with pytest.raises(GdnError, match="multiple of 64"):
+        abi.call("gdn_proj_conv_silu_hip", FAKE, FAKE, FAKE, FAKE, 1, 8, 100, 64, 4, None)
+    with pytest.raises(GdnError, match="conv_k"):
+        abi.call("gdn_proj_conv_silu_hip", FAKE, FAKE, FAKE, FAKE, 1, 8, 128, 64, 5, None)
+
+
+def test_binding_module_api_matches_reference():
+    """Module names, attrs and signatures of the reference's pybind modules."""
+    exts = compile_kernels()
+    assert set(exts) == {"rmsnorm", "proj", "prefill", "decode"}
+    pf = exts["prefill"]
+    assert (pf.H_DIM, pf.K_DIM, pf.V_DIM, pf.C_DIM) == (16, 128, 256, 64)
+    sig = pf.prefill.__doc__.split("(", 1)[1].split(")", 1)[0]
+    assert [a.split(":")[0].strip() for a in sig.split(",")] == \
+        ["q", "k", "v", "A_log", "a", "dt_bias", "b_logits", "mask", "state_in", "scale"]
+    for mod in ("decode", "rmsnorm", "proj"):
+        assert hasattr(exts[mod], "forward")
+
+
+def test_binding_rejects_cpu_tensors():
+    exts = compile_kernels()
+    q = torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        exts["prefill"].prefill(q, q, q, torch.zeros(2), torch.zeros(1, 2, 64, dtype=torch.bfloat16), 0.0,
+                                torch.zeros(1, 2, 64, dtype=torch.bfloat16), torch.ones(1, 64), torch.empty(0), 0.0)
+    with pytest.raises(RuntimeError, match="must be >= 32"):
+        exts["rmsnorm"].forward(torch.zeros(2, 8, dtype=torch.bfloat16), torch.ones(8, dtype=torch.bfloat16),
+                                1e-6, 16, 1)

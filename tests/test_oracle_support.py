@@ -1,0 +1,103 @@
+"""CPU pins for the supporting-kernel oracles and the layer oracle.
+
+* RMSNorm (oracle/rmsnorm_ref.py <- reference/rmsnorm_ref.py:8-28): the
+  reference test's own ground truth, torch.nn.RMSNorm in fp32
+  (tests/test_rmsnorm.py:31-40 of the reference), and a closed form.
+* Projection + conv + SiLU (oracle/proj_ref.py): a brute-force loop, causality.
+* Layer (oracle/layer_ref.py <- gdn_layer.py:108-200): decoding T tokens one at
+  a time equals one prefill over them (the reference's own integration check,
+  bench_gdn.py:200-219).
+"""
+
+import torch
+
+from oracle.layer_ref import GDNLayerBaseline
+from oracle.proj_ref import ref_proj_conv_silu, ref_proj_conv_silu_f32
+from oracle.rmsnorm_ref import ref_rmsnorm
+
+
+def test_rmsnorm_vs_torch_rmsnorm():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 2048, generator=g).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(2048, generator=g)).bfloat16()
+    y = ref_rmsnorm(x, gamma, 1e-6)
+    m = torch.nn.RMSNorm(2048, eps=1e-6, elementwise_affine=True, dtype=torch.float32)
+    with torch.no_grad():
+        m.weight.copy_(gamma.float())
+        y32 = m(x.float())
+    assert y.dtype == torch.bfloat16
+    torch.testing.assert_close(y.float(), y32, rtol=2 ** -7, atol=1e-6)
+
+
+def test_rmsnorm_closed_form_constant_row():
+    x = torch.full((2, 512), 3.0).bfloat16()
+    gamma = torch.full((512,), 2.0).bfloat16()
+    y = ref_rmsnorm(x, gamma, 1e-6)
+    torch.testing.assert_close(y.float(), torch.full((2, 512), 2.0 * 3.0 / (9.0 + 1e-6) ** 0.5), rtol=1e-2, atol=0)
+
+
+def _brute_proj_conv_silu(x, W, cw):
+    B, T, D = x.shape
+    Do, Kc = cw.shape
+    P = torch.zeros(B, T, Do, dtype=torch.float64)
+    for t in range(T):
+        P[:, t] = x[:, t].double() @ W.double().T
+    out = torch.zeros_like(P)
+    for t in range(T):
+        for j in range(Kc):
+            tt = t - (Kc - 1) + j
+            if tt >= 0:
+                out[:, t] += cw[:, j].double() * P[:, tt]
+    return out * torch.sigmoid(out)
+
+
+def test_proj_conv_silu_vs_brute_force():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 9, 64, generator=g).bfloat16()
+    W = (torch.randn(48, 64, generator=g) * 64 ** -0.5).bfloat16()
+    cw = (torch.randn(48, 4, generator=g) * 0.5).bfloat16()
+    ref = _brute_proj_conv_silu(x, W, cw)
+    torch.testing.assert_close(ref_proj_conv_silu_f32(x, W, cw).double(), ref, rtol=1e-2, atol=1e-2)
+    # the reference's own bf16 rounding points stay within bf16 tolerance of the exact value
+    torch.testing.assert_close(ref_proj_conv_silu(x, W, cw).double(), ref, rtol=5e-2, atol=5e-2)
+
+
+def test_proj_conv_silu_is_causal():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(1, 12, 64, generator=g).bfloat16()
+    W = (torch.randn(32, 64, generator=g) * 0.1).bfloat16()
+    cw = torch.randn(32, 4, generator=g).bfloat16()
+    y1 = ref_proj_conv_silu_f32(x, W, cw)
+    x2 = x.clone()
+    x2[:, 7:] = torch.randn(1, 5, 64, generator=g).bfloat16()
+    y2 = ref_proj_conv_silu_f32(x2, W, cw)
+    assert torch.equal(y1[:, :7], y2[:, :7]) and not torch.equal(y1[:, 7:], y2[:, 7:])
+
+
+def _small_weights(D=64, H=2, DK=128, DV=32, CK=4, seed=0):
+    g = torch.Generator().manual_seed(seed)
+
+    def rnd(*s, scale=1.0):
+        return (torch.randn(*s, generator=g) * s[-1] ** -0.5 * scale).bfloat16()
+
+    return dict(norm_gamma=torch.ones(D).bfloat16(),
+                W_q=rnd(H * DK, D, scale=DK ** -0.5), conv_q=(torch.randn(H * DK, CK, generator=g) * 0.5).bfloat16(),
+                W_k=rnd(H * DK, D, scale=DK ** -0.5), conv_k=(torch.randn(H * DK, CK, generator=g) * 0.5).bfloat16(),
+                W_v=rnd(H * DV, D, scale=DK ** -0.5), conv_v=(torch.randn(H * DV, CK, generator=g) * 0.5).bfloat16(),
+                W_a=rnd(H, D), W_b=rnd(H, D), A_log=torch.zeros(H), dt_bias=torch.tensor(0.0),
+                W_o=rnd(D, H * DV))
+
+
+def test_layer_decode_matches_prefill():
+    """Decoding tokens one by one through the baseline layer equals one prefill (bench_gdn.py:200-219)."""
+    w = _small_weights()
+    layer = GDNLayerBaseline(w, chunk_size=16)
+    x = torch.randn(1, 20, 64, generator=torch.Generator().manual_seed(3)).bfloat16()
+    y_pre = layer.forward(x)
+    state = layer.init_decode_state(1)
+    outs = []
+    for t in range(20):
+        y_t, state = layer.decode(x[:, t:t + 1], state)
+        outs.append(y_t)
+    y_dec = torch.cat(outs, 1)
+    torch.testing.assert_close(y_dec.float(), y_pre.float(), rtol=5e-2, atol=2e-2)

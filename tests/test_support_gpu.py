@@ -1,0 +1,88 @@
+"""GPU parity of the supporting kernels: RMSNorm and projection + conv + SiLU.
+
+RMSNorm is checked against the CPU oracle (reference/rmsnorm_ref.py restated)
+and, like the reference's test (tests/test_rmsnorm.py:31-48), against fp32
+torch.nn.RMSNorm.  The projection kernel keeps P in fp32 before the conv (as the
+reference kernel does), so it is held to the fp32 composition within bf16
+output tolerance, and to the reference's bf16-rounded oracle with the
+reference test's max-error bound (tests/test_fused_proj_conv_silu.py:55-59)
+plus a relative term.
+"""
+
+import pytest
+import torch
+
+from oracle.proj_ref import ref_proj_conv_silu, ref_proj_conv_silu_f32
+from oracle.rmsnorm_ref import ref_rmsnorm
+from tests.helpers import assert_out_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B,T", [(1, 1), (1, 2048), (8, 1), (8, 2048), (32, 1), (4, 4096)])
+def test_rmsnorm_reference_shapes(exts, dev, B, T):
+    D = 2048
+    g = torch.Generator().manual_seed(B * 7 + T)
+    x = torch.randn(B * T, D, generator=g).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    y = exts["rmsnorm"].forward(x.to(dev), gamma.to(dev), 1e-6, 256, 2).cpu()
+    y_ref = ref_rmsnorm(x, gamma, 1e-6)
+    # same fp32 math and one final rounding: at most one bf16 ulp apart
+    torch.testing.assert_close(y.float(), y_ref.float(), rtol=2 ** -7, atol=1e-6)
+    m = torch.nn.RMSNorm(D, eps=1e-6, dtype=torch.float32)
+    with torch.no_grad():
+        m.weight.copy_(gamma.float())
+        y32 = m(x.float())
+    diff = (y.float() - y32).abs()
+    assert diff.max().item() < 5e-2 and (diff / (y32.abs() + 1e-8)).max().item() < 0.02
+
+
+@pytest.mark.parametrize("D", [8, 64, 1000 - 1000 % 8, 4096, 16384])
+def test_rmsnorm_generic_D(exts, dev, D):
+    g = torch.Generator().manual_seed(D)
+    x = (3 * torch.randn(37, D, generator=g)).bfloat16()
+    gamma = torch.randn(D, generator=g).bfloat16()
+    y = exts["rmsnorm"].forward(x.to(dev), gamma.to(dev), 1e-5, 64, 1).cpu()
+    torch.testing.assert_close(y.float(), ref_rmsnorm(x, gamma, 1e-5).float(), rtol=2 ** -7, atol=1e-6)
+
+
+def test_rmsnorm_rejects_bad_D(exts, dev):
+    x = torch.zeros(2, 12, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        exts["rmsnorm"].forward(x, torch.ones(12, device=dev, dtype=torch.bfloat16), 1e-6, 256, 2)
+
+
+def _proj_case(B, T, D, Dout, ck=4, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, T, D, generator=g).bfloat16()
+    W = (torch.randn(Dout, D, generator=g) * D ** -0.5).bfloat16()
+    cw = (torch.randn(Dout, ck, generator=g) * 0.5).bfloat16()
+    return x, W, cw
+
+
+@pytest.mark.parametrize("B,T,Dout", [(1, 1, 2048), (1, 64, 2048), (4, 128, 2048), (4, 256, 2048),
+                                      (1, 1, 4096), (4, 64, 4096), (4, 128, 4096)])
+def test_proj_reference_shapes(exts, dev, B, T, Dout):
+    x, W, cw = _proj_case(B, T, 2048, Dout, seed=B * 1000 + T + Dout)
+    y = exts["proj"].forward(x.to(dev), W.to(dev), cw.to(dev)).cpu()
+    assert y.shape == (B, T, Dout) and y.dtype == torch.bfloat16
+    assert_out_close(y, ref_proj_conv_silu_f32(x, W, cw))
+    # The reference's bf16-rounded oracle differs from the fp32 composition by up to a
+    # bf16 ulp of |y| (0.0625 at |y| ~ 8), so its absolute 5e-2 bound gets a relative term.
+    assert_out_close(y, ref_proj_conv_silu(x, W, cw), atol=5e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("T", [2, 3, 124, 125, 126, 250, 251, 1000])
+def test_proj_tile_boundaries(exts, dev, T):
+    """125-token tiles with a 3-token halo: outputs across tile edges must see the previous tile's tokens."""
+    x, W, cw = _proj_case(2, T, 256, 128, seed=T)
+    y = exts["proj"].forward(x.to(dev), W.to(dev), cw.to(dev)).cpu()
+    assert_out_close(y, ref_proj_conv_silu_f32(x, W, cw))
+
+
+@pytest.mark.parametrize("ck", [1, 2, 3, 4])
+@pytest.mark.parametrize("Dout", [48, 2080])
+def test_proj_conv_taps_and_ragged_Dout(exts, dev, ck, Dout):
+    x, W, cw = _proj_case(3, 140, 192, Dout, ck=ck, seed=ck + Dout)
+    y = exts["proj"].forward(x.to(dev), W.to(dev), cw.to(dev)).cpu()
+    assert_out_close(y, ref_proj_conv_silu_f32(x, W, cw))
