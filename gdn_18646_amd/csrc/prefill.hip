@@ -93,7 +93,7 @@ __device__ __forceinline__ int rho_row(int r, int g, int i) { return 32 * (r >> 
 // Kernel 1
 // ---------------------------------------------------------------------------
 constexpr int kKLD = kDK + 8;  // padded LDS row (bf16) for K and Q tiles
-constexpr int kALD = kC + 4;   // padded LDS row (fp32) for A
+constexpr int kAQ = kC / 4 + 4;  // A stored de-interleaved: Ad[i][j % 4][j / 4], padded
 constexpr int kBLD = kC + 8;   // padded LDS row (bf16) for 64x64 tiles
 
 __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p) {
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
 
     __shared__ __attribute__((aligned(16))) bf16 Kl[kC][kKLD];
     __shared__ __attribute__((aligned(16))) bf16 Ql[kC][kKLD];
-    __shared__ __attribute__((aligned(16))) float Am[kC][kALD];
+    __shared__ __attribute__((aligned(16))) float Ad[kC][4][kAQ];
     __shared__ __attribute__((aligned(16))) bf16 Al[kC][kBLD];
     __shared__ __attribute__((aligned(16))) bf16 Tl[kC][kBLD];
     __shared__ float s_lgc[kC], s_bm[kC], s_ms[kC], s_kdec[kC];
@@ -162,89 +162,104 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
     }
     __syncthreads();
 
-    // 3) K K^T and Q K^T: wave w owns row tile w and the column tiles j <= w.
+    // 3) K K^T and Q K^T on the 10 lower 16x16 tiles (i >= j), dealt round
+    //    robin to the 4 waves; the 6 upper tiles of Aq are zeroed.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = 16 * j + m16;
-        if (j > wave) {
+    for (int t = 0; t < 16; ++t) {
+        const int ti = t >> 2, tj = t & 3;  // tile (row ti, col tj)
+        const int order = ti * (ti + 1) / 2 + tj;  // index among lower tiles
+        const int col = 16 * tj + m16;
+        if (tj > ti) {
+            if ((t - 10 + 16) % 4 != wave) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 16 * wave + 4 * g4 + i;
-                Am[row][col] = 0.f;
-                Al[row][col] = f2bf(0.f);
-            }
+            for (int i = 0; i < 4; ++i) Al[16 * ti + 4 * g4 + i][col] = f2bf(0.f);
             continue;
         }
+        if (order % 4 != wave) continue;
         f32x4 accK = {0.f, 0.f, 0.f, 0.f}, accQ = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const bf16x8 aK = *reinterpret_cast<const bf16x8*>(&Kl[16 * wave + m16][32 * s + 8 * g4]);
-            const bf16x8 aQ = *reinterpret_cast<const bf16x8*>(&Ql[16 * wave + m16][32 * s + 8 * g4]);
-            const bf16x8 bK = *reinterpret_cast<const bf16x8*>(&Kl[16 * j + m16][32 * s + 8 * g4]);
+            const bf16x8 aK = *reinterpret_cast<const bf16x8*>(&Kl[16 * ti + m16][32 * s + 8 * g4]);
+            const bf16x8 aQ = *reinterpret_cast<const bf16x8*>(&Ql[16 * ti + m16][32 * s + 8 * g4]);
+            const bf16x8 bK = *reinterpret_cast<const bf16x8*>(&Kl[16 * tj + m16][32 * s + 8 * g4]);
             accK = mfma16x16x32(aK, bK, accK);
             accQ = mfma16x16x32(aQ, bK, accQ);
         }
         const float lgc_col = s_lgc[col];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = 16 * wave + 4 * g4 + i;
+            const int row = 16 * ti + 4 * g4 + i;
             const float d = expf(s_lgc[row] - lgc_col);
-            Am[row][col] = row > col ? s_bm[row] * accK[i] * d : 0.f;
+            Ad[row][col & 3][col >> 2] = row > col ? s_bm[row] * accK[i] * d : 0.f;
             Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
         }
     }
     __syncthreads();
 
-    if (wave == 0) {
-        // 4a) T = (I + A)^-1 by forward substitution, fp32.  Lane c owns
-        // column c: T[i][c] = [i == c] - sum_{j<i} A[i][j] T[j][c]; rows of A
-        // are broadcast reads from LDS.
-        float Tc[kC];
+    // 4) Aq fragments (8) and Kt fragments (16), six per wave.
+    //    Aq (mt, s): lane holds Aq[16mt + m][32s + pi(g, j)].
+    //    Kt (r, s):  lane holds K[32s + pi(g,j)][rho(r, m/4, m%4)] * gamma_C / gamma_t.
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            float acc = (i == lane) ? 1.f : 0.f;
-#pragma unroll
-            for (int j4 = 0; j4 < i; j4 += 4) {
-                const f32x4 arow = *reinterpret_cast<const f32x4*>(&Am[i][j4]);
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (j4 + u < i) acc -= arow[u] * Tc[j4 + u];
-            }
-            Tc[i] = acc;
-        }
-        const float bmc = s_bm[lane];
-#pragma unroll
-        for (int i = 0; i < kC; ++i) Tl[i][lane] = f2bf(Tc[i] * bmc);
-    } else if (wave == 1) {
-        // 4b) Aq fragments (mt, s): lane holds Aq[16mt + m][32s + pi(g, j)].
-#pragma unroll
-        for (int f = 0; f < 8; ++f) {
+    for (int f = 0; f < 24; ++f) {
+        if (f % 4 != wave) continue;
+        if (f < 8) {
             const int mt = f >> 1, s = f & 1;
             const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];
             const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
             const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
             p.wsA[(wc * 8 + f) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
-    } else {
-        // 4c) Kt fragments (r, s): lane holds K[32s + pi(g,j)][rho(r, m/4, m%4)]
-        // times gamma_C / gamma_t.  Waves 2 and 3 take eight fragments each.
-        const int f0 = (wave - 2) * 8;
-#pragma unroll
-        for (int f = f0; f < f0 + 8; ++f) {
-            const int r = f >> 1, s = f & 1;
+        } else {
+            const int fk = f - 8, r = fk >> 1, s = fk & 1;
             const int krow = rho_row(r, m16 >> 2, m16 & 3);
-            bf16x8 frag;
+            bf16x8 fr;
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) {
                 const int t = 32 * s + pi_pos(g4, jj);
-                frag[jj] = f2bf(bf2f(Kl[t][krow]) * s_kdec[t]);
+                fr[jj] = f2bf(bf2f(Kl[t][krow]) * s_kdec[t]);
             }
-            p.wsK[(wc * 16 + f) * 64 + lane] = __builtin_bit_cast(u32x4, frag);
+            p.wsK[(wc * 16 + fk) * 64 + lane] = __builtin_bit_cast(u32x4, fr);
         }
+    }
+
+    // 5) T = (I + A)^-1 by forward substitution, fp32, on all 4 waves: column
+    //    c = 16 wave + lane/4 is owned by a quad; lane sub = lane % 4 keeps
+    //    rows j = 4q + sub of it (Tc[q]) and sums A[i][j] T[j][c] over its j;
+    //    two DPP quad adds give the row's total.
+    {
+        const int c = 16 * wave + (lane >> 2);
+        const int sub = lane & 3;
+        float Tc[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) Tc[q] = 0.f;
+        // Fully unrolled (the row index must be a constant: Tc stays in registers).
+#pragma clang loop unroll(full)
+        for (int i = 0; i < kC; ++i) {
+            float part = 0.f;
+            const int nq = (i + 3) / 4;  // groups touched: q < nq
+#pragma clang loop unroll(full)
+            for (int q4 = 0; q4 < (nq + 3) / 4; ++q4) {
+                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ad[i][sub][4 * q4]);
+#pragma clang loop unroll(full)
+                for (int u = 0; u < 4; ++u) {
+                    const int q = 4 * q4 + u;
+                    if (q < i / 4)
+                        part += a4[u] * Tc[q];
+                    else if (q == i / 4 && (i & 3) != 0)
+                        part += (sub < (i & 3) ? a4[u] : 0.f) * Tc[q];
+                }
+            }
+            part += dpp_f<0xB1>(part);  // quad_perm [1,0,3,2]
+            part += dpp_f<0x4E>(part);  // quad_perm [2,3,0,1]
+            const float val = (i == c ? 1.f : 0.f) - part;
+            if (sub == (i & 3)) Tc[i >> 2] = val;
+        }
+        const float bmc = s_bm[c];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) Tl[4 * q + sub][c] = f2bf(Tc[q] * bmc);
     }
     __syncthreads();
 
-    // 5) Tp fragments, two per wave.
+    // 6) Tp fragments, two per wave.
 #pragma unroll
     for (int f = 2 * wave; f < 2 * wave + 2; ++f) {
         const int mt = f >> 1, s = f & 1;
