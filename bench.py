@@ -49,6 +49,16 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` from profiles/hbm_traffic.json (rocprofv3 --pmc runs), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][kernel]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -85,6 +95,8 @@ def main():
     ap.add_argument("--T", type=int, default=8192)
     ap.add_argument("--B", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 5 device copies of exactly 256 MiB (scale reference for HBM byte counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -100,6 +112,13 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     exts = compile_kernels()
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     B, T, H = args.B, args.T, 16
 
     # ------------------------------------------------------------------ prefill
@@ -253,7 +272,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": state_tflops / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic("gdn_prefill_state_kernel") if (B, T) == (1, 8192) else None,
             "flop_per_launch": STATE_FLOP_PER_TOKEN_HEAD * tokens * H,
             "kernel_ms": ms_state,
         },
@@ -270,7 +289,8 @@ def main():
                        "B": DB, "H": DH, "dk": K, "dv": V},
             "dtype": "fp32",
             "roofline": {"bound": "hbm", "kernel": "gdn_decode_kernel", "achieved": dec_gbs, "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": dec_gbs / PEAK_HBM_GBS, "traffic": None,
+                         "unit": "GB/s", "frac": dec_gbs / PEAK_HBM_GBS,
+                         "traffic": measured_traffic("gdn_decode_kernel"),
                          "bytes_per_launch": decode_bytes(DB, DH), "kernel_ms": ms_decode},
             "cpu_baseline": cpu_decode,
         },
