@@ -22,7 +22,7 @@ BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libgdn_amd.so")
 EXT = os.path.join(PKG, "_gdn_ext" + sysconfig.get_config_var("EXT_SUFFIX"))
 
-HIP_SOURCES = ["abi.cpp", "decode.hip", "prefill.hip", "rmsnorm.hip", "proj.hip"]
+HIP_SOURCES = ["abi.cpp", "decode.hip", "prefill.hip", "rmsnorm.hip", "proj.hip", "layer.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-FP32 VALU forms are disabled on purpose (some give wrong results on
 # the target boxes); the host pass warns that it does not know the feature.

@@ -34,6 +34,8 @@ SIGNATURES = {
                                     _I, _I, _I, _I, _P, _SZ, _P]),
     "gdn_rmsnorm_hip": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "gdn_proj_conv_silu_hip": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "gdn_in_proj_hip": (_I, [_P] * 14 + [_I] * 7 + [_P]),
+    "gdn_decode_conv_step_hip": (_I, [_P] * 10 + [_I] * 5 + [_P]),
 }
 
 STATUS = {0: "GDN_OK", 1: "GDN_ERR_INVALID_ARGUMENT", 2: "GDN_ERR_UNSUPPORTED",

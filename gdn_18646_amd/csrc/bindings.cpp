@@ -232,6 +232,79 @@ Tensor proj_forward(Tensor input, Tensor weight, Tensor conv_w) {
     return out;
 }
 
+// ---------------------------------------------------------------------------
+// layer helpers (no reference counterpart; used by gdn_layer.GDNLayerCustom)
+// ---------------------------------------------------------------------------
+const gdn_bf16_t* opt_bf(const std::optional<Tensor>& t, const char* name, int64_t numel) {
+    if (!t.has_value() || !t->defined() || t->numel() == 0) return nullptr;
+    check_bf16(*t, name);
+    TORCH_CHECK(t->numel() == numel, name, " has ", t->numel(), " elements, expected ", numel);
+    return bf(*t);
+}
+
+// Returns (q, k, v, a, b) head-major, plus new conv caches (q, k, v) when want_cache.
+std::vector<Tensor> in_proj(Tensor xn, Tensor W_qkvab, Tensor conv_w_qkv, int64_t H, int64_t dk, int64_t dv,
+                            std::optional<Tensor> cache_q, std::optional<Tensor> cache_k,
+                            std::optional<Tensor> cache_v, bool want_cache) {
+    check_bf16(xn, "xn");
+    check_bf16(W_qkvab, "W_qkvab");
+    check_bf16(conv_w_qkv, "conv_w_qkv");
+    TORCH_CHECK(xn.dim() == 3, "xn must be [B, T, D]");
+    const int64_t B = xn.size(0), T = xn.size(1), D = xn.size(2);
+    TORCH_CHECK(W_qkvab.dim() == 2 && W_qkvab.size(0) == 2 * H * dk + H * dv + 2 * H && W_qkvab.size(1) == D,
+                "W_qkvab must be [2 H dk + H dv + 2 H, D]");
+    TORCH_CHECK(conv_w_qkv.dim() == 2 && conv_w_qkv.size(0) == 2 * H * dk + H * dv, "conv_w_qkv must be [2 H dk + H dv, K]");
+    const int64_t ck = conv_w_qkv.size(1);
+    const c10::DeviceGuard guard(xn.device());
+    auto o = xn.options();
+    auto q = at::empty({B, H, T, dk}, o), k = at::empty({B, H, T, dk}, o), v = at::empty({B, H, T, dv}, o);
+    auto a = at::empty({B, H, T}, o), b = at::empty({B, H, T}, o);
+    std::vector<Tensor> res = {q, k, v, a, b};
+    gdn_bf16_t *cq = nullptr, *ckk = nullptr, *cv = nullptr;
+    if (want_cache) {
+        auto nq = at::empty({B, H * dk, ck - 1}, o), nk = at::empty({B, H * dk, ck - 1}, o),
+             nv = at::empty({B, H * dv, ck - 1}, o);
+        cq = bf_mut(nq);
+        ckk = bf_mut(nk);
+        cv = bf_mut(nv);
+        res.push_back(nq);
+        res.push_back(nk);
+        res.push_back(nv);
+    }
+    GDN_CHECK_STATUS(gdn_in_proj_hip(bf(xn), bf(W_qkvab), bf(conv_w_qkv), opt_bf(cache_q, "cache_q", B * H * dk * (ck - 1)),
+                                     opt_bf(cache_k, "cache_k", B * H * dk * (ck - 1)),
+                                     opt_bf(cache_v, "cache_v", B * H * dv * (ck - 1)), cq, ckk, cv, bf_mut(q),
+                                     bf_mut(k), bf_mut(v), bf_mut(a), bf_mut(b), B, T, D, H, dk, dv, ck, stream_of(xn)),
+                     "in_proj");
+    return res;
+}
+
+// Decode conv step on P = xn W^T of one token; caches updated in place.
+std::vector<Tensor> decode_conv_step(Tensor P, Tensor conv_w_qkv, Tensor cache_q, Tensor cache_k, Tensor cache_v,
+                                     int64_t H, int64_t dk, int64_t dv) {
+    check_bf16(P, "P");
+    check_bf16(conv_w_qkv, "conv_w_qkv");
+    const int64_t B = P.size(0);
+    TORCH_CHECK(P.dim() == 2 && P.size(1) == 2 * H * dk + H * dv + 2 * H, "P must be [B, 2 H dk + H dv + 2 H]");
+    const int64_t ck = conv_w_qkv.size(1);
+    TORCH_CHECK(conv_w_qkv.dim() == 2 && conv_w_qkv.size(0) == 2 * H * dk + H * dv, "conv_w_qkv must be [2 H dk + H dv, K]");
+    check_bf16(cache_q, "cache_q");
+    check_bf16(cache_k, "cache_k");
+    check_bf16(cache_v, "cache_v");
+    TORCH_CHECK(cache_q.numel() == B * H * dk * (ck - 1) && cache_k.numel() == B * H * dk * (ck - 1) &&
+                    cache_v.numel() == B * H * dv * (ck - 1),
+                "conv caches must be [B, H d, K - 1]");
+    const c10::DeviceGuard guard(P.device());
+    auto o = P.options();
+    auto q = at::empty({B, H, dk}, o), k = at::empty({B, H, dk}, o), v = at::empty({B, H, dv}, o);
+    auto a = at::empty({B, H}, o), b = at::empty({B, H}, o);
+    GDN_CHECK_STATUS(gdn_decode_conv_step_hip(bf(P), bf(conv_w_qkv), bf_mut(cache_q), bf_mut(cache_k), bf_mut(cache_v),
+                                              bf_mut(q), bf_mut(k), bf_mut(v), bf_mut(a), bf_mut(b), B, H, dk, dv, ck,
+                                              stream_of(P)),
+                     "decode_conv_step");
+    return {q, k, v, a, b};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -266,6 +339,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     auto mr = m.def_submodule("rmsnorm", "RMSNorm (bf16)");
     mr.def("forward", &rmsnorm_forward, "RMSNorm forward (bf16, any D % 8 == 0)", py::arg("x"), py::arg("gamma"),
            py::arg("eps"), py::arg("block_threads"), py::arg("rows_per_block"));
+
+    auto ml = m.def_submodule("layer", "Layer-level fused projection and decode conv step");
+    ml.def("in_proj", &in_proj, "Fused q/k/v/a/b projection + conv + SiLU, head-major outputs (+ conv caches)",
+           py::arg("xn"), py::arg("W_qkvab"), py::arg("conv_w_qkv"), py::arg("H"), py::arg("dk"), py::arg("dv"),
+           py::arg("cache_q") = py::none(), py::arg("cache_k") = py::none(), py::arg("cache_v") = py::none(),
+           py::arg("want_cache") = false);
+    ml.def("decode_conv_step", &decode_conv_step, "Decode conv step with projected-token caches (in place)",
+           py::arg("P"), py::arg("conv_w_qkv"), py::arg("cache_q"), py::arg("cache_k"), py::arg("cache_v"),
+           py::arg("H"), py::arg("dk"), py::arg("dv"));
 
     auto mj = m.def_submodule("proj", "Projection + causal conv + SiLU");
     mj.def("forward", &proj_forward, "Fused linear projection + causal depthwise conv1d + SiLU (bf16)",

@@ -28,6 +28,14 @@ constexpr int kOutT = kBM - kHalo;  // 125 outputs per tile
 constexpr int kLD = kBK + 8;        // padded LDS row, bf16
 constexpr int kPLD = kBN + 4;       // padded LDS row, fp32 epilogue
 
+__device__ __forceinline__ int group_of(const gdn_proj::ProjParams& p, int c) {
+    int gi = 0;
+#pragma unroll
+    for (int q = 1; q < gdn_proj::kMaxGroups; ++q)
+        if (q < p.ngroups && c >= p.groups[q].col0) gi = q;
+    return gi;
+}
+
 __global__ __launch_bounds__(256, 2) void gdn_proj_conv_kernel(gdn_proj::ProjParams p) {
     const int tile_t = blockIdx.x, tile_c = blockIdx.y, b = blockIdx.z;
     const int t0 = tile_t * kOutT;
@@ -102,23 +110,40 @@ __global__ __launch_bounds__(256, 2) void gdn_proj_conv_kernel(gdn_proj::ProjPar
     }
 
     // Epilogue: P tile to LDS (the staging buffers are dead after the last barrier).
+    // In the first tile, halo rows of tokens < 0 take the group's cached
+    // projections when it has a cache (x rows there are zero, so P is 0).
+    const int ncache = p.conv_k - 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) Pt[64 * wm + 16 * i + 4 * g4 + e][64 * wn + 16 * j + m16] = acc[i][j][e];
+            for (int e = 0; e < 4; ++e) {
+                const int row = 64 * wm + 16 * i + 4 * g4 + e, col = 64 * wn + 16 * j + m16;
+                float val = acc[i][j][e];
+                if (t0 == 0 && row < kHalo && row >= kHalo - ncache && c0 + col < p.D_out) {
+                    const gdn_proj::ProjGroup& gq = p.groups[group_of(p, c0 + col)];
+                    if (gq.conv && gq.cache_in)
+                        val = bf2f(gq.cache_in[(static_cast<size_t>(b) * gq.width + (c0 + col - gq.col0)) * ncache +
+                                               (row - (kHalo - ncache))]);
+                }
+                Pt[row][col] = val;
+            }
     __syncthreads();
 
     const int cl = tid & (kBN - 1);
     const int c = c0 + cl;
     if (c >= p.D_out) return;
-    int gi = 0;
-#pragma unroll
-    for (int q = 1; q < gdn_proj::kMaxGroups; ++q)
-        if (q < p.ngroups && c >= p.groups[q].col0) gi = q;
-    const gdn_proj::ProjGroup grp = p.groups[gi];
+    const gdn_proj::ProjGroup grp = p.groups[group_of(p, c)];
     const int cc = c - grp.col0;
+    // The workgroup holding the last token refreshes the cache: bf16(P) of
+    // tokens T-ncache .. T-1 (rows of negative tokens hold the old cache).
+    if (grp.conv && grp.cache_out && tid < kBN && t0 + kOutT >= p.T) {
+        for (int j = 0; j < ncache; ++j) {
+            const int tok = p.T - ncache + j;
+            grp.cache_out[(static_cast<size_t>(b) * grp.width + cc) * ncache + j] = f2bf_bits(Pt[tok - t0 + kHalo][cl]);
+        }
+    }
     float w[4] = {0.f, 0.f, 0.f, 0.f};
     if (grp.conv) {
         // Taps aligned to the right: tap conv_k-1 multiplies the current token.
@@ -180,6 +205,6 @@ extern "C" int gdn_proj_conv_silu_hip(const gdn_bf16_t* x, const gdn_bf16_t* W, 
     p.D_out = D_out;
     p.conv_k = conv_k;
     p.ngroups = 1;
-    p.groups[0] = gdn_proj::ProjGroup{0, D_out, 0, 1, 0, out};
+    p.groups[0] = gdn_proj::ProjGroup{0, D_out, 0, 1, 0, out, nullptr, nullptr};
     return gdn_proj::launch_proj(p, static_cast<hipStream_t>(stream));
 }

@@ -13,6 +13,10 @@ constexpr int kMaxGroups = 5;
 // [B, width / head_dim, T, head_dim]; head_dim == 0 writes [B, T, width].
 // conv != 0 applies the causal depthwise conv (weights conv_w rows cw_row0 +
 // column-in-group) and SiLU; conv == 0 stores the current token's P.
+// Conv groups may carry a projected-token cache [B, width, conv_k - 1] (bf16,
+// oldest first): cache_in (nullable) supplies P for the tokens before t = 0
+// (zeros when null), cache_out (nullable) receives bf16(P) of the last
+// conv_k - 1 tokens of the extended sequence cache_in ++ P.
 struct ProjGroup {
     int col0;
     int width;
@@ -20,6 +24,8 @@ struct ProjGroup {
     int conv;
     int cw_row0;
     uint16_t* dst;
+    const uint16_t* cache_in;
+    uint16_t* cache_out;
 };
 
 struct ProjParams {

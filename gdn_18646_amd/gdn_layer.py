@@ -1,0 +1,190 @@
+"""GDN layer on the MI355X kernels — drop-in for the reference's gdn_layer.py.
+
+Same module constants, weight dict, decode-state dict and ``forward`` /
+``decode`` signatures as the reference (gdn_layer.py:24-40, 79-102, 206-316);
+the architecture is read from the weight shapes, so the reference's shape
+(H=16, DK=128, DV=256) and the brief's layer config (DV=128) both run.
+
+Pipeline per call (all GPU, one stream):
+
+  forward  RMSNorm kernel -> one fused q/k/v/a/b in-projection GEMM with the
+           conv + SiLU epilogue writing the prefill kernel's head-major layout
+           (and, on request, the conv cache for decode) -> chunked prefill ->
+           W_o GEMM.  No .item() host sync: dt_bias is read once at
+           construction (call ``refresh()`` after changing the weights).
+  decode   RMSNorm kernel -> xn W^T GEMM -> decode conv step over the cached
+           projections -> decode kernel (state update in place when asked)
+           -> W_o GEMM.
+
+The baseline (pure PyTorch) layer of the reference is the oracle's
+``oracle.layer_ref.GDNLayerBaseline``; it is test infrastructure, not shipped.
+"""
+
+import torch
+
+from . import compile_kernels
+
+# Reference defaults (gdn_layer.py:24-28).
+D = 2048
+H = 16
+DK = 128
+DV = 256
+CONV_K = 4
+
+
+def dims(weights):
+    """(D, H, DK, DV, CONV_K) from a weight dict's shapes."""
+    Hh = weights['A_log'].numel()
+    return (weights['W_q'].shape[1], Hh, weights['W_q'].shape[0] // Hh, weights['W_v'].shape[0] // Hh,
+            weights['conv_q'].shape[1])
+
+
+def _zero_decode_state(weights, B, device=None):
+    """Zeroed decode cache with the reference's keys (gdn_layer.py:31-40)."""
+    Dd, Hh, dk, dv, ck = dims(weights)
+    device = device or weights['norm_gamma'].device
+    bf = torch.bfloat16
+    return dict(
+        recurrent=torch.zeros(B, Hh, dk, dv, dtype=torch.float32, device=device),
+        conv_q=torch.zeros(B, Hh * dk, ck - 1, dtype=bf, device=device),
+        conv_k=torch.zeros(B, Hh * dk, ck - 1, dtype=bf, device=device),
+        conv_v=torch.zeros(B, Hh * dv, ck - 1, dtype=bf, device=device),
+        xn=torch.zeros(B, ck - 1, Dd, dtype=bf, device=device),
+    )
+
+
+def _dt_bias_for_decode(dt_bias, H_=None):
+    """Per-head dt_bias for the decode kernel (gdn_layer.py:72-76)."""
+    if dt_bias.numel() == 1:
+        return dt_bias.reshape(1).expand(H_ or H).contiguous()
+    return dt_bias.contiguous()
+
+
+def make_weights(device="cuda", *, D=D, H=H, DK=DK, DV=DV, CONV_K=CONV_K, std=None, generator=None):
+    """Random weight dict (gdn_layer.py:79-102).
+
+    Default initialisation follows the reference (fan-in scaled normals);
+    ``std`` instead draws every projection and conv weight from N(0, std)
+    (the brief's layer config uses std 0.02).  ``generator`` makes it
+    reproducible (CPU generator; tensors are moved to ``device``).
+    """
+    def rnd(*shape, scale):
+        return (torch.randn(*shape, generator=generator) * scale).to(torch.bfloat16).to(device)
+
+    def proj(rows, cols, extra=1.0):
+        return rnd(rows, cols, scale=std if std is not None else cols ** -0.5 * extra)
+
+    def conv(rows):
+        return rnd(rows, CONV_K, scale=std if std is not None else CONV_K ** -0.5)
+
+    return dict(
+        norm_gamma=torch.ones(D, dtype=torch.bfloat16, device=device),
+        W_q=proj(H * DK, D, DK ** -0.5), conv_q=conv(H * DK),
+        W_k=proj(H * DK, D, DK ** -0.5), conv_k=conv(H * DK),
+        W_v=proj(H * DV, D, DK ** -0.5), conv_v=conv(H * DV),
+        W_a=proj(H, D), W_b=proj(H, D),
+        A_log=torch.zeros(H, dtype=torch.float32, device=device),
+        dt_bias=torch.tensor(0.0, dtype=torch.float32, device=device),
+        W_o=proj(D, H * DV),
+    )
+
+
+class GDNLayerCustom:
+    """Forward/decode of one GDN layer on the HIP kernels (gdn_layer.py:206-316)."""
+
+    def __init__(self, weights, exts=None):
+        self.w = weights
+        self.exts = exts if exts is not None else compile_kernels()
+        self._layer = _layer_module(self.exts)
+        self.D, self.H, self.DK, self.DV, self.CK = dims(weights)
+        self.scale = self.DK ** -0.5
+        self.chunk = int(self.exts['prefill'].C_DIM)
+        self.refresh()
+
+    def refresh(self):
+        """Re-derive the fused weights and gate constants from self.w."""
+        w = self.w
+        self.W_qkvab = torch.cat([w['W_q'], w['W_k'], w['W_v'], w['W_a'], w['W_b']], 0).contiguous()
+        self.conv_qkv = torch.cat([w['conv_q'], w['conv_k'], w['conv_v']], 0).contiguous()
+        self.A_log = w['A_log'].float().contiguous()
+        dtb = w['dt_bias'].float()
+        self.dt_bias_scalar = float(dtb.reshape(-1)[0].item()) if dtb.numel() == 1 else None
+        self.dt_bias_vec = _dt_bias_for_decode(dtb, self.H).float().contiguous()
+        self.W_o = w['W_o'].contiguous()
+
+    def init_decode_state(self, B, device=None):
+        return _zero_decode_state(self.w, B, device=device)
+
+    def _rmsnorm(self, x2d):
+        return self.exts['rmsnorm'].forward(x2d.contiguous(), self.w['norm_gamma'], 1e-6, 256, 2)
+
+    @torch.no_grad()
+    def forward(self, x, mask=None, return_state=False, state=None):
+        """x [B, T, D] bf16 -> y [B, T, D] bf16.
+
+        mask [B, T] fp32 (1 keep, 0 masked; default all ones).  With
+        ``return_state`` also returns the decode-state dict after the last
+        token (recurrent state and conv caches), so decode can continue the
+        sequence.  ``state`` (optional) continues from an earlier state
+        (initial recurrent state and conv caches).
+        """
+        if self.dt_bias_scalar is None:
+            raise ValueError("prefill takes a scalar dt_bias (as the reference kernel)")
+        B, T, _ = x.shape
+        Dd, Hh, dk, dv = self.D, self.H, self.DK, self.DV
+        if mask is None:
+            mask = torch.ones(B, T, dtype=torch.float32, device=x.device)
+        xn = self._rmsnorm(x.reshape(B * T, Dd)).reshape(B, T, Dd)
+        st = state or {}
+        outs = self._layer.in_proj(xn, self.W_qkvab, self.conv_qkv, Hh, dk, dv,
+                                   st.get('conv_q'), st.get('conv_k'), st.get('conv_v'), bool(return_state))
+        q, k, v, a, b = outs[:5]
+        s_in = st.get('recurrent')
+        if s_in is None:
+            s_in = torch.empty(0, dtype=torch.float32, device=x.device)
+        o, S = self.exts['prefill'].prefill(q, k, v, self.A_log, a, self.dt_bias_scalar, b, mask.contiguous(),
+                                            s_in, self.scale)
+        y = o.transpose(1, 2).reshape(B, T, Hh * dv) @ self.W_o.T
+        if not return_state:
+            return y
+        nc = self.CK - 1
+        xn_hist = torch.cat([st.get('xn', torch.zeros(B, nc, Dd, dtype=x.dtype, device=x.device)), xn], 1)[:, -nc:]
+        return y, dict(recurrent=S, conv_q=outs[5], conv_k=outs[6], conv_v=outs[7], xn=xn_hist.contiguous())
+
+    @torch.no_grad()
+    def decode(self, x, state=None, inplace=False):
+        """One token: x [B, 1, D] -> (y [B, 1, D], new state dict).
+
+        The conv caches of the state dict hold the last CONV_K-1 projected
+        tokens (the reference baseline's decode semantics).  With
+        ``inplace=True`` the state tensors are updated in place and the same
+        dict is returned (no allocation of a new 4-D state per step).
+        """
+        B, T, _ = x.shape
+        assert T == 1, f"decode expects T=1, got T={T}"
+        Dd, Hh, dk, dv = self.D, self.H, self.DK, self.DV
+        if state is None:
+            state = self.init_decode_state(B, device=x.device)
+        xn = self._rmsnorm(x.reshape(B, Dd))
+        P = xn @ self.W_qkvab.T
+        if inplace:
+            cq, ck, cv, S_out = state['conv_q'], state['conv_k'], state['conv_v'], state['recurrent']
+        else:
+            cq, ck, cv = (state[n].clone() for n in ('conv_q', 'conv_k', 'conv_v'))
+            S_out = torch.empty_like(state['recurrent'])
+        q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv)
+        o = torch.empty(B, Hh, dv, dtype=torch.float32, device=x.device)
+        self.exts['decode'].forward(q, k, v, a, b, self.A_log, self.dt_bias_vec, state['recurrent'], self.scale,
+                                    o, S_out)
+        y = o.to(x.dtype).reshape(B, 1, Hh * dv) @ self.W_o.T
+        xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
+        if inplace:
+            state['xn'] = xn_hist.contiguous()
+            return y, state
+        return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist.contiguous())
+
+
+def _layer_module(exts):
+    """The binding's layer submodule (kept beside the four reference modules)."""
+    from . import native_extension
+    return native_extension().layer

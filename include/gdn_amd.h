@@ -17,6 +17,8 @@
  *   gdn_rmsnorm_hip           <- rmsnorm_forward_impl / launch_rmsnorm,
  *                                kernels/rmsnorm.cu:112-131,251-276
  *   gdn_proj_conv_silu_hip    <- fused_proj_conv_silu, kernels/fused_proj_conv_silu.cu:298-355
+ *   gdn_in_proj_hip           <- GDNLayerCustom.forward's projections, gdn_layer.py:240-252
+ *   gdn_decode_conv_step_hip  <- _decode_conv_step / _decode_fused_proj_step, gdn_layer.py:43-69
  */
 #ifndef GDN_AMD_H
 #define GDN_AMD_H
@@ -152,6 +154,37 @@ int gdn_rmsnorm_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, gdn_bf16_t* y,
 int gdn_proj_conv_silu_hip(const gdn_bf16_t* x, const gdn_bf16_t* W,
                            const gdn_bf16_t* conv_w, gdn_bf16_t* out,
                            int B, int T, int D, int D_out, int conv_k, void* stream);
+
+/*
+ * Layer in-projection for a prefill: P = xn [B, T, D] x W^T with
+ * W = [W_q; W_k; W_v; W_a; W_b] ([2 H dk + H dv + 2 H, D] bf16), causal
+ * depthwise conv (conv_w_qkv [2 H dk + H dv, conv_k]) + SiLU on the q/k/v
+ * columns, written head-major: q, k [B, H, T, dk]; v [B, H, T, dv];
+ * a, b [B, H, T] (no conv).  Optional conv caches [B, H d, conv_k - 1] bf16
+ * of projected tokens (oldest first): *_in (NULL = zeros) precede t = 0,
+ * *_out (NULL = not written, must not alias *_in) receive the last conv_k - 1
+ * projected tokens.  D % 64 == 0, conv_k in 1..4.
+ * Replaces the three fused_proj_conv_silu launches, the a/b GEMMs and the
+ * transposes of GDNLayerCustom.forward (gdn_layer.py:240-252).
+ */
+int gdn_in_proj_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv,
+                    const gdn_bf16_t* cache_q_in, const gdn_bf16_t* cache_k_in, const gdn_bf16_t* cache_v_in,
+                    gdn_bf16_t* cache_q_out, gdn_bf16_t* cache_k_out, gdn_bf16_t* cache_v_out,
+                    gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
+                    int B, int T, int D, int H, int dk, int dv, int conv_k, void* stream);
+
+/*
+ * Decode-step conv: P [B, 2 H dk + H dv + 2 H] bf16 holds xn W^T of the new
+ * token (columns q|k|v|a|b).  q/k/v columns go through the causal conv over
+ * the cached previous conv_k - 1 projections (cache_* [B, H d, conv_k - 1],
+ * updated in place) and SiLU; a/b pass through.  Outputs in the decode
+ * kernel's layouts: q, k [B, H, dk]; v [B, H, dv]; a, b [B, H].
+ * Replaces _decode_conv_step / _decode_fused_proj_step (gdn_layer.py:43-69).
+ */
+int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* conv_w_qkv,
+                             gdn_bf16_t* cache_q, gdn_bf16_t* cache_k, gdn_bf16_t* cache_v,
+                             gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
+                             int B, int H, int dk, int dv, int conv_k, void* stream);
 
 #ifdef __cplusplus
 }

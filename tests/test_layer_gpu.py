@@ -1,0 +1,107 @@
+"""GPU tests of the layer (gdn_18646_amd.gdn_layer) against the oracle's
+baseline layer (oracle.layer_ref <- gdn_layer.py:108-200) and the reference's
+own layer checks (bench_gdn.py:152-219).
+
+Tolerances: the reference's layer check, |dy| < 5e-2 + 0.1 |y_ref|
+(bench_gdn.py:159-161), for outputs that pass through bf16 projections
+computed with different rounding points; recurrent states 1e-2 relative
+Frobenius; GPU-vs-GPU consistency checks use the brief's 2e-2.
+"""
+
+import pytest
+import torch
+
+from gdn_18646_amd.gdn_layer import GDNLayerCustom, make_weights
+from oracle.layer_ref import GDNLayerBaseline
+from tests.helpers import assert_out_close, assert_state_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(dev, D=256, H=2, DK=128, DV=64, std=None, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    w = make_weights(device="cpu", D=D, H=H, DK=DK, DV=DV, std=std, generator=g)
+    w["A_log"] = torch.full((H,), -0.3)
+    w["dt_bias"] = torch.tensor(0.1)
+    w["norm_gamma"] = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    return w, {k: v.to(dev) for k, v in w.items()}
+
+
+def _layer_close(y, y_ref, what):
+    assert_out_close(y, y_ref, atol=5e-2, rtol=0.1, what=what)
+
+
+def test_layer_forward_matches_baseline(dev):
+    w_cpu, w = _weights(dev)
+    x = torch.randn(2, 150, 256, generator=torch.Generator().manual_seed(1)).bfloat16()
+    mask = torch.ones(2, 150)
+    mask[1, 100:] = 0
+    y = GDNLayerCustom(w).forward(x.to(dev), mask.to(dev))
+    y_ref = GDNLayerBaseline(w_cpu, chunk_size=64).forward(x, mask)
+    _layer_close(y.cpu(), y_ref, "layer forward")
+
+
+def test_layer_decode_matches_baseline(dev):
+    w_cpu, w = _weights(dev, seed=2)
+    layer, base = GDNLayerCustom(w), GDNLayerBaseline(w_cpu)
+    st, st_ref = layer.init_decode_state(3), base.init_decode_state(3)
+    g = torch.Generator().manual_seed(3)
+    for _ in range(8):
+        x = torch.randn(3, 1, 256, generator=g).bfloat16()
+        y, st = layer.decode(x.to(dev), st)
+        y_ref, st_ref = base.decode(x, st_ref)
+        _layer_close(y.cpu(), y_ref, "decode output")
+    assert_state_close(st["recurrent"].cpu(), st_ref["recurrent"])
+    for key in ("conv_q", "conv_k", "conv_v"):
+        assert_out_close(st[key].cpu(), st_ref[key], what=key)
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_layer_decode_matches_prefill(dev, inplace):
+    """Decoding T tokens one at a time equals one prefill (bench_gdn.py:200-219)."""
+    _, w = _weights(dev, seed=4)
+    layer = GDNLayerCustom(w)
+    x = torch.randn(2, 64, 256, generator=torch.Generator().manual_seed(5)).bfloat16().to(dev)
+    y_pre = layer.forward(x)
+    st = layer.init_decode_state(2)
+    ys = []
+    for t in range(64):
+        y_t, st = layer.decode(x[:, t:t + 1], st, inplace=inplace)
+        ys.append(y_t)
+    assert_out_close(torch.cat(ys, 1), y_pre, what="decode vs prefill")
+
+
+def test_prefill_hands_off_to_decode(dev):
+    """forward(x[:t], return_state) then decode tokens t.. == forward(x) (cache hand-off)."""
+    _, w = _weights(dev, seed=6)
+    layer = GDNLayerCustom(w)
+    x = torch.randn(2, 80, 256, generator=torch.Generator().manual_seed(7)).bfloat16().to(dev)
+    y_full = layer.forward(x)
+    y_a, st = layer.forward(x[:, :70], return_state=True)
+    ys = [y_a]
+    for t in range(70, 80):
+        y_t, st = layer.decode(x[:, t:t + 1], st)
+        ys.append(y_t)
+    assert_out_close(torch.cat(ys, 1), y_full, what="prefill + decode vs prefill")
+    # and prefill continuing from a state equals one prefill
+    y_b, _ = layer.forward(x[:, 70:], return_state=True, state=layer.forward(x[:, :70], return_state=True)[1])
+    assert_out_close(torch.cat([y_a, y_b], 1), y_full, what="prefill + prefill vs prefill")
+
+
+def test_layer_config5_shapes(dev):
+    """Brief config 5 dims (hidden 2048, H=16, d=128, conv 4, std 0.02): a short
+    slice against the baseline, then the full B=4 x T=4096 prefill and 128 decode steps."""
+    g = torch.Generator().manual_seed(8)
+    w_cpu = make_weights(device="cpu", D=2048, H=16, DK=128, DV=128, std=0.02, generator=g)
+    w = {k: v.to(dev) for k, v in w_cpu.items()}
+    layer = GDNLayerCustom(w)
+    xs = torch.randn(1, 192, 2048, generator=g).bfloat16()
+    _layer_close(layer.forward(xs.to(dev)).cpu(), GDNLayerBaseline(w_cpu, chunk_size=64).forward(xs), "cfg5 slice")
+
+    x = torch.randn(4, 4096, 2048, generator=g).bfloat16().to(dev)
+    y, st = layer.forward(x, return_state=True)
+    assert y.shape == (4, 4096, 2048) and torch.isfinite(y.float()).all()
+    for _ in range(128):
+        y_t, st = layer.decode(torch.randn(4, 1, 2048, device=dev).bfloat16(), st, inplace=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y_t.float()).all() and torch.isfinite(st["recurrent"]).all()
