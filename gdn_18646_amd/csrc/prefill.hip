@@ -30,6 +30,8 @@
 //                32-wide k-step, the order produced by two stacked accumulators
 //   rho(r,g,i) = 32(r/2) + 8g + 4(r%2) + i          state row held in
 //                accumulator tile r, slot i, of lane group g
+#include <algorithm>
+
 #include "gdn_common.hpp"
 
 namespace {
@@ -273,18 +275,31 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
 // ---------------------------------------------------------------------------
 // Kernel 2
 // ---------------------------------------------------------------------------
-// Per-chunk operands staged in LDS (one buffer; the kernel double-buffers).
+// Per-chunk operands staged in LDS (one buffer; the kernels double-buffer).
 // Every block is a run of 1 KiB "fragments": 64 lanes x 16 bytes, lane l's
 // 16 bytes at offset 16 l, i.e. exactly one MFMA operand register quad.
 constexpr int kFragB = 1024;
-constexpr int kOffK = 0;                   // 16 fragments (mt, s): K rows 16mt+m, k 32s+8g..+7
-constexpr int kOffQ = kOffK + 16 * kFragB;  // 16 fragments, same order for Q
-constexpr int kOffT = kOffQ + 16 * kFragB;  // 8 fragments of Tp
-constexpr int kOffA = kOffT + 8 * kFragB;   // 8 fragments of Aq
-constexpr int kOffKt = kOffA + 8 * kFragB;  // 16 fragments of Kt
-constexpr int kOffG = kOffKt + 16 * kFragB; // gates: gamma[64], m scale gamma[64] (1 KiB slot)
-constexpr int kOffV = kOffG + kFragB;       // per wave: V[64][16] bf16 (2 KiB)
-__host__ __device__ constexpr int state_buf_bytes(int nw) { return kOffV + nw * 2 * kFragB; }
+enum { kModeOut = 0, kModeMap = 1 };
+
+// Staging layout of one buffer.  The map pass (no outputs) stages neither Q
+// nor Aq.  V is per wave: [64 rows][16 NT columns] bf16.
+template <int MODE, int NW, int NT>
+struct Stage {
+    static constexpr bool out = MODE == kModeOut;
+    static constexpr int offK = 0;                                  // 16: (mt, s) -> K rows 16mt+m, k 32s+8g
+    static constexpr int offQ = offK + 16 * kFragB;                 // 16 (out only)
+    static constexpr int offT = offQ + (out ? 16 : 0) * kFragB;     // 8: Tp (mt, s)
+    static constexpr int offA = offT + 8 * kFragB;                  // 6 (out only): Aq slots used
+    static constexpr int offKt = offA + (out ? 6 : 0) * kFragB;     // 16: Kt (r, s)
+    static constexpr int offG = offKt + 16 * kFragB;                // gamma[64], m scale gamma[64]
+    static constexpr int offV = offG + kFragB;
+    static constexpr int vWave = 2 * NT * kFragB;
+    static constexpr int bytes = offV + NW * vWave;
+    static constexpr int stores = out ? 16 * NT : 0;                // output stores per chunk per wave
+};
+
+// Aq workspace fragments (mt, s) read by the output: (0,0),(1,0),(2,0),(2,1),(3,0),(3,1).
+__device__ __forceinline__ constexpr int aq_slot(int i) { return i < 2 ? 2 * i : i + 2; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -298,7 +313,7 @@ typedef __attribute__((address_space(3))) uint16_t lds_u16;
 // must be uniform over the wave.  Asynchronous: completion is vmcnt.  Issued
 // as inline asm so the compiler's wait-count pass does not drain the copy
 // before unrelated LDS reads of the other buffer (it cannot prove they do not
-// alias); the kernel orders copies with its own vmcnt waits and barriers.
+// alias); the kernels order copies with their own vmcnt waits and barriers.
 // M0 is otherwise unused on gfx950 (LDS instructions do not read it), so the
 // clobber is safe here.
 #pragma clang diagnostic push
@@ -315,270 +330,418 @@ __device__ __forceinline__ void dma16(const void* g, lds_u8* lds_base) {
 // vmcnt wait that precedes it.)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// s_waitcnt immediates (gfx9 layout: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
-__device__ __forceinline__ void wait_vm16() { __builtin_amdgcn_s_waitcnt(0x4F70); }  // vmcnt(16)
-// A full chunk issues exactly this many output stores per wave after the
-// next chunk's copies; vector memory ops complete in issue order, so waiting
-// for vmcnt <= kStoresPerChunk means the copies have landed.
-constexpr int kStoresPerChunk = 16;
+// vmcnt(N) with the other counters open (gfx9 layout: vmcnt[3:0] | expcnt[6:4]
+// | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).  Vector memory ops retire in issue
+// order, so vmcnt(N) means "all but the last N issued have completed".
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
 // Per-lane byte offsets of the staging copies, fixed for the whole kernel.
 struct StageLane {
     uint32_t kq;  // K/Q fragment: row (lane & 15), k offset 8 (lane >> 4)
     uint32_t fr;  // workspace fragment: 16 lane
     uint32_t g;   // gate block: 16 (lane & 31)
-    uint32_t v;   // V tile: row (lane >> 1), 8 columns (lane & 1)
+    uint32_t v;   // V tile: row lane / (2 NT), 8 columns (lane % (2 NT))
 };
 
 // Stage chunk operands into `buf`.  Full chunks use uniform bases plus the
 // lane offsets; the last, partial chunk clamps rows to the sequence (so no
 // load leaves the tensors) and its padded rows are zeroed after arrival.
-template <int NW>
+// Shared jobs are dealt round robin to the NW waves; each wave copies its own
+// V tile when `stage_v`.
+template <int MODE, int NW, int NT>
 __device__ __forceinline__ void stage_chunk(const PrefillParams& p, lds_u8* buf, size_t row_base, int nvalid,
-                                            size_t wc, int wave, int lane, int col0_wave, const StageLane& L) {
+                                            size_t wc, int wave, int lane, int col0_wave, bool stage_v,
+                                            const StageLane& L) {
+    using St = Stage<MODE, NW, NT>;
     const unsigned char* tb = reinterpret_cast<const unsigned char*>(p.wsT + wc * 8 * 64);
     const unsigned char* ab = reinterpret_cast<const unsigned char*>(p.wsA + wc * 8 * 64);
     const unsigned char* ktb = reinterpret_cast<const unsigned char*>(p.wsK + wc * 16 * 64);
     const unsigned char* gb = reinterpret_cast<const unsigned char*>(p.wsG + wc * 128);
+    constexpr int kRowsPerV = 32 / NT;  // V rows per 1 KiB copy
     if (nvalid == kC) {
         const unsigned char* kb = reinterpret_cast<const unsigned char*>(p.k + row_base * kDK);
         const unsigned char* qb = reinterpret_cast<const unsigned char*>(p.q + row_base * kDK);
 #pragma unroll
         for (int f = 0; f < 16; ++f) {
             const uint32_t o = L.kq + (f >> 2) * 16 * kDK * 2 + (f & 3) * 64;
-            if (f % NW == wave) dma16(kb + o, buf + kOffK + f * kFragB);
-            if ((f + 16) % NW == wave) dma16(qb + o, buf + kOffQ + f * kFragB);
+            if (f % NW == wave) dma16(kb + o, buf + St::offK + f * kFragB);
+            if (St::out && (f + 16) % NW == wave) dma16(qb + o, buf + St::offQ + f * kFragB);
         }
+        if (stage_v) {
 #pragma unroll
-        for (int it = 0; it < 2; ++it)
-            dma16(reinterpret_cast<const unsigned char*>(p.v + (row_base + 32 * it) * p.dv) + L.v,
-                  buf + kOffV + wave * 2 * kFragB + it * kFragB);
+            for (int it = 0; it < 2 * NT; ++it)
+                dma16(reinterpret_cast<const unsigned char*>(p.v + (row_base + kRowsPerV * it) * p.dv) + L.v,
+                      buf + St::offV + wave * St::vWave + it * kFragB);
+        }
     } else {
         const int m = lane & 15, g = lane >> 4;
 #pragma unroll
         for (int f = 0; f < 16; ++f) {
             const int row = min(16 * (f >> 2) + m, nvalid - 1);
             const size_t e = (row_base + row) * kDK + 32 * (f & 3) + 8 * g;
-            if (f % NW == wave) dma16(p.k + e, buf + kOffK + f * kFragB);
-            if ((f + 16) % NW == wave) dma16(p.q + e, buf + kOffQ + f * kFragB);
+            if (f % NW == wave) dma16(p.k + e, buf + St::offK + f * kFragB);
+            if (St::out && (f + 16) % NW == wave) dma16(p.q + e, buf + St::offQ + f * kFragB);
         }
+        if (stage_v) {
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int row = min(32 * it + (lane >> 1), nvalid - 1);
-            dma16(p.v + (row_base + row) * p.dv + col0_wave + 8 * (lane & 1), buf + kOffV + wave * 2 * kFragB + it * kFragB);
+            for (int it = 0; it < 2 * NT; ++it) {
+                const int row = min(kRowsPerV * it + lane / (2 * NT), nvalid - 1);
+                dma16(p.v + (row_base + row) * p.dv + col0_wave + 8 * (lane % (2 * NT)),
+                      buf + St::offV + wave * St::vWave + it * kFragB);
+            }
         }
     }
 #pragma unroll
-    for (int f = 0; f < 8; ++f) {
-        if ((f + 32) % NW == wave) dma16(tb + f * kFragB + L.fr, buf + kOffT + f * kFragB);
-        if ((f + 40) % NW == wave) dma16(ab + f * kFragB + L.fr, buf + kOffA + f * kFragB);
+    for (int f = 0; f < 8; ++f)
+        if ((f + 32) % NW == wave) dma16(tb + f * kFragB + L.fr, buf + St::offT + f * kFragB);
+    if (St::out) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+            if ((i + 40) % NW == wave) dma16(ab + aq_slot(i) * kFragB + L.fr, buf + St::offA + i * kFragB);
     }
 #pragma unroll
     for (int f = 0; f < 16; ++f)
-        if ((f + 48) % NW == wave) dma16(ktb + f * kFragB + L.fr, buf + kOffKt + f * kFragB);
-    if (64 % NW == wave) dma16(gb + L.g, buf + kOffG);
+        if ((f + 48) % NW == wave) dma16(ktb + f * kFragB + L.fr, buf + St::offKt + f * kFragB);
+    if (64 % NW == wave) dma16(gb + L.g, buf + St::offG);
 }
 
 // Zero the rows >= nvalid of the staged K, Q and V (partial chunk only).
-template <int NW>
+template <int MODE, int NW, int NT>
 __device__ __forceinline__ void zero_pad_rows(lds_u8* buf, int nvalid, int wave, int lane) {
+    using St = Stage<MODE, NW, NT>;
     const u32x4 z = {0u, 0u, 0u, 0u};
-    if (16 * 0 + (lane & 15) >= 0) {
 #pragma unroll
-        for (int f = 0; f < 32; ++f)
-            if (f % NW == wave && 16 * ((f & 15) >> 2) + (lane & 15) >= nvalid)
-                *reinterpret_cast<lds_u32x4*>(buf + kOffK + f * kFragB + 16 * lane) = z;  // K then Q (contiguous)
-    }
+    for (int f = 0; f < (St::out ? 32 : 16); ++f)
+        if (f % NW == wave && 16 * ((f & 15) >> 2) + (lane & 15) >= nvalid)
+            *reinterpret_cast<lds_u32x4*>(buf + St::offK + f * kFragB + 16 * lane) = z;  // K then Q (contiguous)
 #pragma unroll
-    for (int it = 0; it < 2; ++it)
-        if (32 * it + (lane >> 1) >= nvalid)
-            *reinterpret_cast<lds_u32x4*>(buf + kOffV + wave * 2 * kFragB + it * kFragB + 16 * lane) = z;
+    for (int it = 0; it < 2 * NT; ++it)
+        if ((32 / NT) * it + lane / (2 * NT) >= nvalid)
+            *reinterpret_cast<lds_u32x4*>(buf + St::offV + wave * St::vWave + it * kFragB + 16 * lane) = z;
 }
 
 __device__ __forceinline__ bf16x8 frag(const lds_u8* buf, int off, int lane) {
     return *reinterpret_cast<const lds_bf16x8*>(buf + off + 16 * lane);
 }
 
-// One chunk of the state recurrence for a 128 x 16 column tile, operands in LDS.
-// `ob` points at out[row_base][0] (uniform).  All operand fragments are read
-// from LDS up front (none depends on the state), so the MFMA chain that does
-// depend on it never waits on LDS in between.
-__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8], uint16_t* ob, int dv, int nvalid,
-                                            int wave, int lane, int col) {
-    const int n = lane & 15, g = lane >> 4;
-    const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + kOffG);
-    const lds_u16* Vs = reinterpret_cast<const lds_u16*>(buf + kOffV + wave * 2 * kFragB);
+// bf16 of (x - bf16(x)) for a pair of accumulator quads: the low half of a
+// two-term bf16 split.
+__device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const bf16x8 h) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = f2bf(lo[i] - bf2f(h[i]));
+        r[4 + i] = f2bf(hi[i] - bf2f(h[4 + i]));
+    }
+    return r;
+}
 
-    bf16x8 kf[16], qf[16], tf[8], af[6], ktf[16];
+// One chunk of the state recurrence for a 128 x (16 NT) column tile, operands
+// in LDS.  `ob` points at out[row_base][0] (uniform).  All operand fragments
+// are read from LDS up front (none depends on the state), so the MFMA chain
+// that does depend on it never waits on LDS in between.  `v_zero`: the tile
+// has no V (identity columns of the map pass).
+template <int MODE, int NW, int NT>
+__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
+                                            int wave, int lane, int col0_wave, bool v_zero) {
+    using St = Stage<MODE, NW, NT>;
+    const int n = lane & 15, g = lane >> 4;
+    const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + St::offG);
+    const lds_u16* Vs = reinterpret_cast<const lds_u16*>(buf + St::offV + wave * St::vWave);
+
+    bf16x8 kf[16], qf[St::out ? 16 : 1], tf[8], af[St::out ? 6 : 1], ktf[16];
 #pragma unroll
     for (int f = 0; f < 16; ++f) {
-        kf[f] = frag(buf, kOffK + f * kFragB, lane);
-        qf[f] = frag(buf, kOffQ + f * kFragB, lane);
+        kf[f] = frag(buf, St::offK + f * kFragB, lane);
+        if constexpr (St::out) qf[f] = frag(buf, St::offQ + f * kFragB, lane);
     }
 #pragma unroll
-    for (int f = 0; f < 8; ++f) tf[f] = frag(buf, kOffT + f * kFragB, lane);
-    af[0] = frag(buf, kOffA + 0 * kFragB, lane);
-    af[1] = frag(buf, kOffA + 2 * kFragB, lane);
-    af[2] = frag(buf, kOffA + 4 * kFragB, lane);
-    af[3] = frag(buf, kOffA + 5 * kFragB, lane);
-    af[4] = frag(buf, kOffA + 6 * kFragB, lane);
-    af[5] = frag(buf, kOffA + 7 * kFragB, lane);
+    for (int f = 0; f < 8; ++f) tf[f] = frag(buf, St::offT + f * kFragB, lane);
+    if constexpr (St::out) {
 #pragma unroll
-    for (int f = 0; f < 16; ++f) ktf[f] = frag(buf, kOffKt + f * kFragB, lane);
-    float vv[16];
+        for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offA + i * kFragB, lane);
+    }
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int f = 0; f < 16; ++f) ktf[f] = frag(buf, St::offKt + f * kFragB, lane);
+    float vv[NT][16];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[4 * mt + i] = bf2f(Vs[(16 * mt + 4 * g + i) * 16 + n]);
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                vv[nt][4 * mt + i] = v_zero ? 0.f : bf2f(Vs[(16 * mt + 4 * g + i) * 16 * NT + 16 * nt + n]);
     f32x4 gam[4], co[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
         gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
-        co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
+        if constexpr (St::out) co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
     }
     const float gC = G[kC - 1];
 
-    // (a) X = K S, P = Q S.
-    f32x4 X[4], P[4];
+    // (a) X = K S (and P = Q S for the output).
+    f32x4 X[4][NT], P[4][NT];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) X[mt] = P[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const bf16x8 Bs = pack8(S[2 * s], S[2 * s + 1]);
+        bf16x8 Bs[NT];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            X[mt] = mfma16x16x32(kf[4 * mt + s], Bs, X[mt]);
-            P[mt] = mfma16x16x32(qf[4 * mt + s], Bs, P[mt]);
-        }
+        for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                X[mt][nt] = mfma16x16x32(kf[4 * mt + s], Bs[nt], X[mt][nt]);
+                if constexpr (St::out) P[mt][nt] = mfma16x16x32(qf[4 * mt + s], Bs[nt], P[mt][nt]);
+            }
     }
     // (b) Y = V - gamma o X (in place in X).
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) X[mt][i] = vv[4 * mt + i] - gam[mt][i] * X[mt][i];
-    // (c) dV = Tp Y.
-    f32x4 D[4];
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) D[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < 4; ++i) X[mt][nt][i] = vv[nt][4 * mt + i] - gam[mt][i] * X[mt][nt][i];
+    // (c) dV = Tp Y.
+    f32x4 D[4][NT];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-        const bf16x8 BY = pack8(X[2 * s], X[2 * s + 1]);
+        bf16x8 BY[NT];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) D[mt] = mfma16x16x32(tf[2 * mt + s], BY, D[mt]);
+        for (int nt = 0; nt < NT; ++nt) BY[nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) D[mt][nt] = mfma16x16x32(tf[2 * mt + s], BY[nt], D[mt][nt]);
     }
-    const bf16x8 BD0 = pack8(D[0], D[1]);
-    const bf16x8 BD1 = pack8(D[2], D[3]);
+    bf16x8 BD0[NT], BD1[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        BD0[nt] = pack8(D[0][nt], D[1][nt]);
+        BD1[nt] = pack8(D[2][nt], D[3][nt]);
+    }
     // (e) S <- gamma_C S + Kt dV  (issued before (d): it is the recurrence's critical path).
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        S[r] *= gC;
-        S[r] = mfma16x16x32(ktf[2 * r], BD0, S[r]);
-        S[r] = mfma16x16x32(ktf[2 * r + 1], BD1, S[r]);
-    }
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            S[r][nt] *= gC;
+            S[r][nt] = mfma16x16x32(ktf[2 * r], BD0[nt], S[r][nt]);
+            S[r][nt] = mfma16x16x32(ktf[2 * r + 1], BD1[nt], S[r][nt]);
+        }
+    if constexpr (!St::out) return;
     // (d) O = (m scale gamma) o P + Aq dV -> bf16.
-    f32x4 O[4];
-    O[0] = mfma16x16x32(af[0], BD0, co[0] * P[0]);
-    O[1] = mfma16x16x32(af[1], BD0, co[1] * P[1]);
-    O[2] = mfma16x16x32(af[3], BD1, mfma16x16x32(af[2], BD0, co[2] * P[2]));
-    O[3] = mfma16x16x32(af[5], BD1, mfma16x16x32(af[4], BD0, co[3] * P[3]));
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        if (nvalid == kC) {
+    for (int nt = 0; nt < NT; ++nt) {
+        f32x4 O[4];
+        O[0] = mfma16x16x32(af[0], BD0[nt], co[0] * P[0][nt]);
+        O[1] = mfma16x16x32(af[1], BD0[nt], co[1] * P[1][nt]);
+        O[2] = mfma16x16x32(af[3], BD1[nt], mfma16x16x32(af[2], BD0[nt], co[2] * P[2][nt]));
+        O[3] = mfma16x16x32(af[5], BD1[nt], mfma16x16x32(af[4], BD0[nt], co[3] * P[3][nt]));
+        const int col = col0_wave + 16 * nt + n;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ob[(16 * mt + 4 * g + i) * dv + col] = f2bf_bits(O[mt][i]);
-        } else {
+        for (int mt = 0; mt < 4; ++mt) {
+            if (nvalid == kC) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 16 * mt + 4 * g + i;
-                if (row < nvalid) ob[row * dv + col] = f2bf_bits(O[mt][i]);
+                for (int i = 0; i < 4; ++i) ob[(16 * mt + 4 * g + i) * dv + col] = f2bf_bits(O[mt][i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 16 * mt + 4 * g + i;
+                    if (row < nvalid) ob[row * dv + col] = f2bf_bits(O[mt][i]);
+                }
             }
         }
     }
 }
 
-// One workgroup = NW waves = NW column tiles of 16 of one (sequence, head).
-// The chunk operands are shared by the waves and double-buffered in LDS: the
-// copies for chunk c+1 are in flight while chunk c is computed.
-template <int NW>
-__global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParams p, int nvg, int nheads,
-                                                                    int xcd_map) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][state_buf_bytes(NW)];
+// Work decomposition of the state pass.
+struct StateGrid {
+    int nvg;      // workgroups per (head, group)
+    int ngroups;  // chunk groups per sequence (G)
+    int nheads;   // sequences x heads
+    int xcd_map;  // deal the workgroups of one (head, group) to one XCD
+    float* psi;   // map pass: zero-state results, [nheads][G][dv/16][64][32] fp32
+    uint16_t* phi;  // map pass: transitions, [nheads][G][128][128] bf16 row-major
+};
+
+// State pass over one chunk group per workgroup (NW waves, NT 16-column tiles
+// each, of one (sequence, head)).
+//   kModeOut: from the group's initial state (state_in composed through the
+//             earlier groups' maps), writes the outputs; the last group writes
+//             state_out.
+//   kModeMap: columns [0, dv) start from zero (psi), columns [dv, dv + 128)
+//             from the identity with V = 0 (phi = the group's transition).
+// With one group (G = 1) only the output pass runs.  The chunk operands are
+// shared by the waves and double-buffered in LDS: the copies for chunk c+1
+// are in flight while chunk c is computed.
+template <int MODE, int NW, int NT>
+__global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParams p, StateGrid sg) {
+    using St = Stage<MODE, NW, NT>;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][St::bytes];
     lds_u8* const buf0 = (lds_u8*)&smem[0][0];
     lds_u8* const buf1 = (lds_u8*)&smem[1][0];
 
-    // blockIdx -> (head, column group).  With xcd_map the column groups of a
-    // head land on one XCD (workgroups are dealt to the 8 XCDs round robin),
-    // so the operands they all read share that XCD's L2.
     const int wg = blockIdx.x;
-    int head, vg;
-    if (xcd_map) {
+    const int nunits = sg.nheads * sg.ngroups;
+    int unit, vg;
+    if (sg.xcd_map) {
         const int xcd = wg & 7, j = wg >> 3;
-        vg = j % nvg;
-        head = (j / nvg) * 8 + xcd;
+        vg = j % sg.nvg;
+        unit = (j / sg.nvg) * 8 + xcd;
     } else {
-        vg = wg % nvg;
-        head = wg / nvg;
+        vg = wg % sg.nvg;
+        unit = wg / sg.nvg;
     }
-    if (head >= nheads) return;  // uniform over the workgroup
+    if (unit >= nunits) return;  // uniform over the workgroup
+    const int head = unit / sg.ngroups, grp = unit % sg.ngroups;
     const int sidx = head / p.H;
     const int h = head % p.H;
     const SeqInfo sq = seq_info(p, sidx);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;
+    const int n = lane & 15, g = lane >> 4;
     const int dv = p.dv;
-    const int col0_wave = (vg * NW + wave) * 16;
-    const int col = col0_wave + (lane & 15);
+    const int col0_wave = (vg * NW + wave) * 16 * NT;  // map pass: >= dv means identity columns
+    const bool phi_cols = MODE == kModeMap && col0_wave >= dv;
+    const int nchunks = (sq.len + kC - 1) / kC;
+    const int glen = (nchunks + sg.ngroups - 1) / sg.ngroups;
+    const int c_begin = min(grp * glen, nchunks), c_end = min(c_begin + glen, nchunks);
     const StageLane L = {static_cast<uint32_t>((lane & 15) * kDK * 2 + (lane >> 4) * 16),
                          static_cast<uint32_t>(16 * lane), static_cast<uint32_t>(16 * (lane & 31)),
-                         static_cast<uint32_t>((lane >> 1) * dv * 2 + (lane & 1) * 16 + col0_wave * 2)};
+                         static_cast<uint32_t>((lane / (2 * NT)) * dv * 2 + (lane % (2 * NT)) * 16 +
+                                               (phi_cols ? 0 : col0_wave) * 2)};
 
-    // State tile: S[r][i] = S[rho(r, g, i)][col].
-    f32x4 S[8];
-    if (p.state_in) {
-        const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+    // State tile: S[r][nt][i] = S[rho(r, g, i)][col0_wave + 16 nt + n].
+    f32x4 S[8][NT];
+    if constexpr (MODE == kModeMap) {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) S[r][i] = sin[rho_row(r, g, i) * dv + col];
-    } else {
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int r = 0; r < 8; ++r) S[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int i = 0; i < 4; ++i)
+                    S[r][nt][i] = (phi_cols && rho_row(r, g, i) == col0_wave - dv + 16 * nt + n) ? 1.f : 0.f;
+    } else {
+        if (p.state_in) {
+            const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) S[r][nt][i] = sin[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        // Initial state of this group: S <- phi_j S + psi_j for the earlier
+        // groups j, in order.  phi in bf16 against S split into two bf16
+        // terms (S_hi + S_lo), fp32 accumulation on top of psi.
+        for (int j = 0; j < grp; ++j) {
+            const uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK;
+            bf16x8 Bh[4][NT], Bl[4][NT];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    Bh[s][nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
+                    Bl[s][nt] = pack8_lo(S[2 * s][nt], S[2 * s + 1][nt], Bh[s][nt]);
+                }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f32x4* Ps = reinterpret_cast<const f32x4*>(
+                    sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * (dv / 16) + col0_wave / 16 + nt) * 2048 +
+                    lane * 32);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(
+                        Ph + rho_row(r, n >> 2, n & 3) * kDK + 32 * s + 8 * g));
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        S[r][nt] = mfma16x16x32(a, Bh[s][nt], S[r][nt]);
+                        S[r][nt] = mfma16x16x32(a, Bl[s][nt], S[r][nt]);
+                    }
+                }
+        }
     }
 
-    const int nchunks = (sq.len + kC - 1) / kC;
     const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
     auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
     auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
     auto wcof = [&](int c) { return static_cast<size_t>(sq.slot0 + c) * p.H + h; };
     auto step = [&](int c, lds_u8* cur, lds_u8* nxt) {
         // Chunk c's copies were issued before chunk c-1's output stores.
-        if (c == 0)
-            wait_vm0();
+        if (c == c_begin)
+            wait_vm<0>();
         else
-            wait_vm16();
+            wait_vm<St::stores>();
         lds_barrier();  // chunk c staged by every wave; nobody still reads `nxt`
-        if (c + 1 < nchunks) stage_chunk<NW>(p, nxt, rows(c + 1), nval(c + 1), wcof(c + 1), wave, lane, col0_wave, L);
+        if (c + 1 < c_end)
+            stage_chunk<MODE, NW, NT>(p, nxt, rows(c + 1), nval(c + 1), wcof(c + 1), wave, lane, col0_wave,
+                                      !phi_cols, L);
         const int nv = nval(c);
         if (nv < kC) {
-            zero_pad_rows<NW>(cur, nv, wave, lane);
+            zero_pad_rows<MODE, NW, NT>(cur, nv, wave, lane);
             lds_barrier();
         }
-        state_chunk(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col);
+        state_chunk<MODE, NW, NT>(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col0_wave, phi_cols);
     };
 
-    if (nchunks > 0) stage_chunk<NW>(p, buf0, rows(0), nval(0), wcof(0), wave, lane, col0_wave, L);
-    for (int c = 0; c < nchunks; c += 2) {
+    if (c_begin < c_end)
+        stage_chunk<MODE, NW, NT>(p, buf0, rows(c_begin), nval(c_begin), wcof(c_begin), wave, lane, col0_wave,
+                                  !phi_cols, L);
+    for (int c = c_begin; c < c_end; c += 2) {
         step(c, buf0, buf1);
-        if (c + 1 < nchunks) step(c + 1, buf1, buf0);
+        if (c + 1 < c_end) step(c + 1, buf1, buf0);
     }
 
-    float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+    if constexpr (MODE == kModeOut) {
+        if (grp != sg.ngroups - 1) return;
+        float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
+        for (int r = 0; r < 8; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col] = S[r][i];
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n] = S[r][nt][i];
+    } else if (phi_cols) {
+        uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + grp) * kDK * kDK;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    Ph[rho_row(r, g, i) * kDK + col0_wave - dv + 16 * nt + n] = f2bf_bits(S[r][nt][i]);
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            f32x4* Ps = reinterpret_cast<f32x4*>(
+                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp) * (dv / 16) + col0_wave / 16 + nt) * 2048 +
+                lane * 32);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) Ps[r] = S[r][nt];
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -600,18 +763,50 @@ constexpr size_t kBytesG = 128 * 4;
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-struct WsLayout {
-    size_t offT, offA, offK, offG, total;
+// How the state pass is split: NT 16-column tiles per wave; NW waves per
+// workgroup; G chunk groups per sequence when (sequence, head) pairs alone
+// cannot fill the chip (each group then runs its own chain of chunks, joined
+// through the groups' affine maps).
+struct StatePlan {
+    int NT, NW_out, nvg_out, NW_map, nvg_map, G;
 };
 
-WsLayout ws_layout(long long slots, int H) {
+// `exact`: max_chunks is the exact chunk count of every sequence, so the
+// group count is trimmed until no group is empty.  Workspace sizing uses the
+// untrimmed count, which never decreases as sequences grow.
+StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact) {
+    StatePlan s;
+    s.NT = (dv % 32 == 0) ? 2 : 1;
+    const int tiles = dv / (16 * s.NT);
+    s.NW_out = (tiles % 4 == 0) ? 4 : (tiles % 2 == 0) ? 2 : 1;
+    s.nvg_out = tiles / s.NW_out;
+    const int mtiles = (dv + kDK) / (16 * s.NT);
+    // At most 4 waves: with 8 a wave is held to 256 registers and spills.
+    s.NW_map = (mtiles % 4 == 0) ? 4 : (mtiles % 2 == 0) ? 2 : 1;
+    s.nvg_map = mtiles / s.NW_map;
+    const long long base = nheads * s.nvg_out;  // output-pass workgroups with one group
+    long long G = 1;
+    if (base < 256 && max_chunks >= 8) G = std::min<long long>(std::min<long long>(16, 256 / base), max_chunks / 4);
+    if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
+    s.G = G < 2 ? 1 : static_cast<int>(G);
+    return s;
+}
+
+struct WsLayout {
+    size_t offT, offA, offK, offG, offPsi, offPhi, total;
+};
+
+WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const StatePlan& sp) {
     const size_t ch = static_cast<size_t>(slots) * H;
     WsLayout L;
     L.offT = 0;
     L.offA = align256(L.offT + ch * kBytesT);
     L.offK = align256(L.offA + ch * kBytesA);
     L.offG = align256(L.offK + ch * kBytesK);
-    L.total = align256(L.offG + ch * kBytesG);
+    L.offPsi = align256(L.offG + ch * kBytesG);
+    const size_t units = sp.G > 1 ? static_cast<size_t>(nheads) * sp.G : 0;
+    L.offPhi = align256(L.offPsi + units * kDK * dv * 4);
+    L.total = align256(L.offPhi + units * kDK * kDK * 2);
     return L;
 }
 
@@ -624,11 +819,29 @@ int check_common(const char* who, int H, int dk, int dv) {
     return GDN_OK;
 }
 
-// phases: bit 0 = chunk-parallel intra kernel, bit 1 = sequential state kernel.
-int launch(PrefillParams& p, int nseq, int nchunk_grid, void* workspace, size_t ws_bytes,
+template <int MODE, int NT>
+int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_t stream) {
+    const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups * sg.nvg;
+    if (nwg > 0x7fffffffLL) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
+    const dim3 grid(static_cast<unsigned>(nwg));
+    switch (NW) {
+        case 1: hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 1, NT>), grid, dim3(64), 0, stream, p, sg); break;
+        case 2: hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 2, NT>), grid, dim3(128), 0, stream, p, sg); break;
+        case 4: hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 4, NT>), grid, dim3(256), 0, stream, p, sg); break;
+        default:
+            return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
+    }
+    return gdn_host::check_launch(MODE == kModeMap ? "gdn_prefill_state_kernel<map>" : "gdn_prefill_state_kernel");
+}
+
+// phases: bit 0 = chunk-parallel intra kernel, bit 1 = state pass (map pass
+// when chunk groups are used, then the output pass).
+int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* workspace, size_t ws_bytes,
            long long slots, hipStream_t stream, int phases) {
     using gdn_host::fail;
-    const WsLayout L = ws_layout(slots, p.H);
+    const long long nheads = static_cast<long long>(nseq) * p.H;
+    const StatePlan sp = plan_state(nheads, p.dv, nchunk_grid, exact);
+    const WsLayout L = ws_layout(slots, p.H, nheads, p.dv, sp);
     if (!workspace || ws_bytes < L.total)
         return fail(GDN_ERR_WORKSPACE, "prefill: workspace of %zu bytes given, %zu needed", ws_bytes, L.total);
     if (!gdn_host::aligned(workspace, 256))
@@ -645,24 +858,22 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, void* workspace, size_t 
         if (st != GDN_OK) return st;
     }
     if (!(phases & 2)) return GDN_OK;
-    const int nheads = nseq * p.H;
-    const long long waves = static_cast<long long>(nheads) * (p.dv / 16);
-    // Waves per workgroup: one while the grid is smaller than the CU count
-    // (latency-bound, each wave gets a CU), more to share LDS staging after.
-    int NW = waves <= 256 ? 1 : (waves <= 512 ? 2 : 4);
-    while ((p.dv / 16) % NW) NW >>= 1;
-    const int nvg = p.dv / (16 * NW);
-    const int xcd_map = (nheads % 8 == 0) ? 1 : 0;
-    const long long nwg = static_cast<long long>(nheads) * nvg;
-    if (nwg > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-    const dim3 grid(static_cast<unsigned>(nwg));
-    if (NW == 4)
-        hipLaunchKernelGGL(gdn_prefill_state_kernel<4>, grid, dim3(256), 0, stream, p, nvg, nheads, xcd_map);
-    else if (NW == 2)
-        hipLaunchKernelGGL(gdn_prefill_state_kernel<2>, grid, dim3(128), 0, stream, p, nvg, nheads, xcd_map);
-    else
-        hipLaunchKernelGGL(gdn_prefill_state_kernel<1>, grid, dim3(64), 0, stream, p, nvg, nheads, xcd_map);
-    return gdn_host::check_launch("gdn_prefill_state_kernel");
+    StateGrid sg = {};
+    sg.ngroups = sp.G;
+    sg.nheads = static_cast<int>(nheads);
+    sg.psi = reinterpret_cast<float*>(ws + L.offPsi);
+    sg.phi = reinterpret_cast<uint16_t*>(ws + L.offPhi);
+    sg.xcd_map = ((nheads * sp.G) % 8 == 0) ? 1 : 0;
+    int st;
+    if (sp.G > 1) {
+        sg.nvg = sp.nvg_map;
+        st = sp.NT == 2 ? launch_state<kModeMap, 2>(p, sg, sp.NW_map, stream)
+                        : launch_state<kModeMap, 1>(p, sg, sp.NW_map, stream);
+        if (st != GDN_OK) return st;
+    }
+    sg.nvg = sp.nvg_out;
+    return sp.NT == 2 ? launch_state<kModeOut, 2>(p, sg, sp.NW_out, stream)
+                      : launch_state<kModeOut, 1>(p, sg, sp.NW_out, stream);
 }
 
 }  // namespace
@@ -671,18 +882,20 @@ extern "C" {
 
 size_t gdn_prefill_workspace_bytes(int B, int H, int T, int dk, int dv) {
     (void)dk;
-    (void)dv;
-    if (B <= 0 || H <= 0 || T <= 0) return 0;
-    const long long slots = static_cast<long long>(B) * ((T + kC - 1) / kC);
-    return ws_layout(slots, H).total;
+    if (B <= 0 || H <= 0 || T <= 0 || dv <= 0) return 0;
+    const long long nch = (T + kC - 1) / kC;
+    const long long slots = static_cast<long long>(B) * nch;
+    const long long nheads = static_cast<long long>(B) * H;
+    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, nch, false)).total;
 }
 
 size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int dk, int dv) {
     (void)dk;
-    (void)dv;
-    if (num_seqs <= 0 || H <= 0 || T_total < 0) return 0;
+    if (num_seqs <= 0 || H <= 0 || T_total < 0 || dv <= 0) return 0;
     const long long slots = static_cast<long long>(T_total) / kC + num_seqs + 1;
-    return ws_layout(slots, H).total;
+    const long long nheads = static_cast<long long>(num_seqs) * H;
+    // The group count only grows with the longest sequence: size for T_total.
+    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, (T_total + kC - 1) / kC, false)).total;
 }
 
 }  // extern "C"
@@ -737,7 +950,7 @@ int prefill_batch(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
                            state_out, static_cast<size_t>(B) * H * dk * dv);
         return gdn_host::check_launch("gdn_fill_zero_kernel");
     }
-    return launch(p, B, p.chunks_per_seq, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream),
+    return launch(p, B, p.chunks_per_seq, true, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream),
                   phases);
 }
 
@@ -809,7 +1022,7 @@ int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_b
     const int maxlen = (max_seqlen > 0 && max_seqlen < T_total) ? max_seqlen : T_total;
     const int nchunk_grid = (maxlen + kC - 1) / kC;
     const long long slots = static_cast<long long>(T_total) / kC + num_seqs + 1;
-    return launch(p, num_seqs, nchunk_grid, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream), 3);
+    return launch(p, num_seqs, nchunk_grid, false, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream), 3);
 }
 
 }  // extern "C"

@@ -125,6 +125,44 @@ def test_prefill_state_composition_full_size(exts, dev):
     assert_state_close(S2, S, tol=5e-3)
 
 
+@pytest.mark.parametrize("B,H,T,dv,masked", [(1, 1, 4000, 16, False), (1, 2, 1500, 64, True),
+                                              (2, 1, 2600, 48, True)])
+def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
+    """Few (sequence, head) pairs and long sequences: the state pass splits each
+    sequence into chunk groups and joins them through the groups' affine maps
+    (6 to 13 groups here, with 16- and 32-column tiles).  Slow decay (A_log = -8,
+    about 0.9998 per token) so the state carried into each group matters: a wrong
+    transition map would show at O(1)."""
+    d = synth.prefill_inputs(B, T, H, 128, dv, seed=T + dv, state=True)
+    d["A_log"] = torch.linspace(-8.0, -2.0, H)
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(T)
+        mask = (torch.rand(B, T, generator=g) > 0.2).float()
+        mask[0, 640:768] = 0.0  # two whole masked chunks
+    out, S = _kernel(exts, d, dev, mask=mask, state_in=d["state_in"])
+    o_ref, S_ref = _oracle(d, mask=mask, state_in=d["state_in"])
+    assert_out_close(out, o_ref)
+    assert_state_close(S, S_ref)
+
+
+def test_prefill_varlen_chunk_groups(exts, dev):
+    """Packed sequences of very different lengths with chunk groups: the short
+    ones leave most of their groups empty (identity maps).  Slow decay, as above."""
+    lengths = [3000, 10, 700, 0, 1500]
+    d = synth.varlen_inputs(lengths, 2, 128, 64, seed=11)
+    d["A_log"] = torch.tensor([-8.0, -3.0])
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    out, S = exts["prefill"].prefill_varlen(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"],
+                                            g["cu_seqlens"], g["state_in"], 0.0)
+    torch.cuda.synchronize()
+    o_ref, S_ref = ref_prefill_varlen(d["q"], d["k"], d["v"], d["A_log"], d["a"], 0.0, d["b_logits"],
+                                      d["cu_seqlens"], state_in=d["state_in"], chunk_size=64)
+    assert_out_close(out.cpu(), o_ref)
+    for i in range(len(lengths)):
+        assert_state_close(S[i].cpu(), S_ref[i], what=f"state of sequence {i}")
+
+
 def test_prefill_varlen_config4(exts, dev):
     """Brief config 4: 8 packed sequences, lengths U[512, 8192] (seed 3), nonzero initial states."""
     lengths = synth.varlen_lengths(8, 512, 8192, seed=3)
