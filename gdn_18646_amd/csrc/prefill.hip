@@ -1,4 +1,4 @@
-// GDN chunked prefill (chunk C = 64, dk = 128), two kernels.
+// GDN chunked prefill (chunk C = 64, dk = 128).
 //
 // Reference: kernels/prefill_chunked.cu:41-417 (one fused block per (b,h),
 // WMMA for two products, the rest scalar) with the semantics of
@@ -12,18 +12,23 @@
 // Kernel 1, gdn_prefill_intra_kernel — one 256-thread workgroup per
 // (chunk, head, sequence); every chunk in parallel.  Builds K K^T and Q K^T on
 // bf16 MFMA, the decay matrix, the fp32 forward substitution for T, and writes
-// per chunk (bf16 unless noted), already in the register order kernel 2's
-// MFMA operands need (one 16-byte load per lane per fragment):
+// per chunk (bf16 unless noted), already in the register order the state
+// kernels' MFMA operands need (one 16-byte load per lane per fragment):
 //   Tp  = T diag(beta m)                       8 fragments  (8 KiB)
 //   Aq  = m scale (Q K^T o Gamma), t >= s      8 fragments  (8 KiB)
 //   Kt  = (K o gamma_C/gamma)^T                16 fragments (16 KiB)
 //   G   = [gamma_t, m_t scale gamma_t]         128 fp32
-// Kernel 2, gdn_prefill_state_kernel — one wave per (sequence, head, 16*NT
-// state columns) walks the chunks in order.  The fp32 state tile lives in
-// MFMA accumulator registers the whole time; its bf16 copy feeds the next
+// Kernel 2, gdn_prefill_state_kernel — each wave owns 16*NT state columns of
+// one (sequence, head) and walks chunks in order.  The fp32 state tile lives
+// in MFMA accumulator registers the whole time; its bf16 copy feeds the next
 // chunk's products directly (no LDS), because the k order inside an MFMA
 // operand is free: the state rows are assigned to accumulator slots so that
 // the accumulator of the state update IS the B operand of K S and Q S.
+// When (sequence, head) pairs alone cannot fill the chip, each sequence is cut
+// into G chunk groups (S maps affinely across a group: S_out = phi S_in + psi):
+//   map pass   (kernel 2, map mode)  psi and phi of every group but the last,
+//   scan       (gdn_prefill_scan_kernel)  S_in of every group, in order,
+//   output pass (kernel 2, output mode) every group from its S_in, in parallel.
 //
 // Fragment k-order conventions (lane l: m = l%16 row/column, g = l/16 group):
 //   pi(g, j)   = j < 4 ? 4g + j : 16 + 4g + (j-4)   chunk position inside a
@@ -568,21 +573,24 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 
 // Work decomposition of the state pass.
 struct StateGrid {
-    int nvg;      // workgroups per (head, group)
-    int ngroups;  // chunk groups per sequence (G)
-    int nheads;   // sequences x heads
-    int xcd_map;  // deal the workgroups of one (head, group) to one XCD
-    float* psi;   // map pass: zero-state results, [nheads][G][dv/16][64][32] fp32
-    uint16_t* phi;  // map pass: transitions, [nheads][G][128][128] bf16 row-major
+    int nvg;         // workgroups per (head, group)
+    int ngroups;     // chunk groups per sequence (G)
+    int ngroups_run; // groups per sequence this launch covers (map pass: G - 1)
+    int nheads;      // sequences x heads
+    int xcd_map;     // deal the workgroups of one (head, group) to one XCD
+    float* psi;      // [nheads][G][dv/16][64][32] fp32: map pass zero-state results, then
+                     // (scan) the initial state of group j + 1 in slot j
+    uint16_t* phi;   // map pass: transitions, [nheads][G][128][128] bf16 row-major
 };
 
 // State pass over one chunk group per workgroup (NW waves, NT 16-column tiles
 // each, of one (sequence, head)).
-//   kModeOut: from the group's initial state (state_in composed through the
-//             earlier groups' maps), writes the outputs; the last group writes
+//   kModeOut: from the group's initial state (state_in for group 0, else the
+//             scan's result), writes the outputs; the last group writes
 //             state_out.
 //   kModeMap: columns [0, dv) start from zero (psi), columns [dv, dv + 128)
 //             from the identity with V = 0 (phi = the group's transition).
+//             The last group's map is never needed and is not computed.
 // With one group (G = 1) only the output pass runs.  The chunk operands are
 // shared by the waves and double-buffered in LDS: the copies for chunk c+1
 // are in flight while chunk c is computed.
@@ -594,7 +602,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
     lds_u8* const buf1 = (lds_u8*)&smem[1][0];
 
     const int wg = blockIdx.x;
-    const int nunits = sg.nheads * sg.ngroups;
+    const int nunits = sg.nheads * sg.ngroups_run;
     int unit, vg;
     if (sg.xcd_map) {
         const int xcd = wg & 7, j = wg >> 3;
@@ -605,7 +613,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
         unit = wg / sg.nvg;
     }
     if (unit >= nunits) return;  // uniform over the workgroup
-    const int head = unit / sg.ngroups, grp = unit % sg.ngroups;
+    const int head = unit / sg.ngroups_run, grp = unit % sg.ngroups_run;
     const int sidx = head / p.H;
     const int h = head % p.H;
     const SeqInfo sq = seq_info(p, sidx);
@@ -633,55 +641,29 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     S[r][nt][i] = (phi_cols && rho_row(r, g, i) == col0_wave - dv + 16 * nt + n) ? 1.f : 0.f;
+    } else if (grp > 0) {
+        // Initial state of this group, left by the scan in psi slot grp - 1.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const f32x4* Ps = reinterpret_cast<const f32x4*>(
+                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048 +
+                lane * 32);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r];
+        }
+    } else if (p.state_in) {
+        const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) S[r][nt][i] = sin[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n];
     } else {
-        if (p.state_in) {
-            const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
+        for (int r = 0; r < 8; ++r)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) S[r][nt][i] = sin[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n];
-        } else {
-#pragma unroll
-            for (int r = 0; r < 8; ++r)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        // Initial state of this group: S <- phi_j S + psi_j for the earlier
-        // groups j, in order.  phi in bf16 against S split into two bf16
-        // terms (S_hi + S_lo), fp32 accumulation on top of psi.
-        for (int j = 0; j < grp; ++j) {
-            const uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK;
-            bf16x8 Bh[4][NT], Bl[4][NT];
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    Bh[s][nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
-                    Bl[s][nt] = pack8_lo(S[2 * s][nt], S[2 * s + 1][nt], Bh[s][nt]);
-                }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const f32x4* Ps = reinterpret_cast<const f32x4*>(
-                    sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * (dv / 16) + col0_wave / 16 + nt) * 2048 +
-                    lane * 32);
-#pragma unroll
-                for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r];
-            }
-#pragma unroll
-            for (int r = 0; r < 8; ++r)
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(
-                        Ph + rho_row(r, n >> 2, n & 3) * kDK + 32 * s + 8 * g));
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) {
-                        S[r][nt] = mfma16x16x32(a, Bh[s][nt], S[r][nt]);
-                        S[r][nt] = mfma16x16x32(a, Bl[s][nt], S[r][nt]);
-                    }
-                }
-        }
+            for (int nt = 0; nt < NT; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
@@ -741,6 +723,86 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 #pragma unroll
             for (int r = 0; r < 8; ++r) Ps[r] = S[r][nt];
         }
+    }
+}
+
+// Initial states of the chunk groups: S_in(0) = state_in (or 0) and
+// S_in(j + 1) = phi_j S_in(j) + psi_j, written over psi_j.  One workgroup per
+// (sequence-head, 16-column tile); wave w owns state rows 32w .. 32w + 31 (row
+// tiles 2w and 2w + 1 of the accumulator order), which are exactly the rows of
+// MFMA k-step w, so each wave publishes its rows as that k-step's B operand
+// (bf16 high and low halves of the fp32 state) and reads all four back.  The
+// transitions and zero-state results of step j + 1 are loaded during step j.
+__global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(PrefillParams p, StateGrid sg) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][8 * kFragB];
+    const int dv = p.dv, ntile = dv / 16;
+    const int nunits = sg.nheads * ntile;
+    int u = blockIdx.x;
+    if (u >= nunits) return;
+    if (nunits % 8 == 0) u = (u & 7) * (nunits >> 3) + (u >> 3);  // one head's tiles on one XCD
+    const int head = u / ntile, tile = u % ntile;
+    const int sidx = head / p.H, h = head % p.H;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15, g = lane >> 4;
+    const int col = 16 * tile + n;
+
+    f32x4 S[2];
+    if (p.state_in) {
+        const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[rr][i] = sin[rho_row(2 * wave + rr, g, i) * dv + col];
+    } else {
+        S[0] = S[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int steps = sg.ngroups - 1;
+    auto psi_at = [&](int j) {
+        return reinterpret_cast<f32x4*>(sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048 +
+                                        lane * 32) + 2 * wave;
+    };
+    auto load = [&](int j, bf16x8 (&A)[2][4], f32x4 (&Y)[2]) {
+        const uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                A[rr][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(
+                    Ph + rho_row(2 * wave + rr, n >> 2, n & 3) * kDK + 32 * ks + 8 * g));
+            Y[rr] = psi_at(j)[rr];
+        }
+    };
+    auto step = [&](int j, lds_u8* buf, const bf16x8 (&A)[2][4], const f32x4 (&Y)[2], bf16x8 (&An)[2][4],
+                    f32x4 (&Yn)[2]) {
+        const bf16x8 hi = pack8(S[0], S[1]);
+        *reinterpret_cast<lds_bf16x8*>(buf + (2 * wave) * kFragB + 16 * lane) = hi;
+        *reinterpret_cast<lds_bf16x8*>(buf + (2 * wave + 1) * kFragB + 16 * lane) = pack8_lo(S[0], S[1], hi);
+        lds_barrier();
+        if (j + 1 < steps) load(j + 1, An, Yn);
+        f32x4 acc[2] = {Y[0], Y[1]};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const bf16x8 bh = frag(buf, (2 * ks) * kFragB, lane);
+            const bf16x8 bl = frag(buf, (2 * ks + 1) * kFragB, lane);
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                acc[rr] = mfma16x16x32(A[rr][ks], bh, acc[rr]);
+                acc[rr] = mfma16x16x32(A[rr][ks], bl, acc[rr]);
+            }
+        }
+        f32x4* out = psi_at(j);
+        out[0] = S[0] = acc[0];
+        out[1] = S[1] = acc[1];
+    };
+    bf16x8 A0[2][4], A1[2][4];
+    f32x4 Y0[2], Y1[2];
+    if (steps > 0) load(0, A0, Y0);
+    lds_u8* const buf0 = (lds_u8*)&smem[0][0];
+    lds_u8* const buf1 = (lds_u8*)&smem[1][0];
+    for (int j = 0; j < steps; j += 2) {
+        step(j, buf0, A0, Y0, A1, Y1);
+        if (j + 1 < steps) step(j + 1, buf1, A1, Y1, A0, Y0);
     }
 }
 
@@ -835,7 +897,7 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
 }
 
 // phases: bit 0 = chunk-parallel intra kernel, bit 1 = state pass (map pass
-// when chunk groups are used, then the output pass).
+// and scan when chunk groups are used, then the output pass).
 int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* workspace, size_t ws_bytes,
            long long slots, hipStream_t stream, int phases) {
     using gdn_host::fail;
@@ -863,15 +925,23 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     sg.nheads = static_cast<int>(nheads);
     sg.psi = reinterpret_cast<float*>(ws + L.offPsi);
     sg.phi = reinterpret_cast<uint16_t*>(ws + L.offPhi);
-    sg.xcd_map = ((nheads * sp.G) % 8 == 0) ? 1 : 0;
     int st;
     if (sp.G > 1) {
         sg.nvg = sp.nvg_map;
+        sg.ngroups_run = sp.G - 1;
+        sg.xcd_map = ((nheads * sg.ngroups_run) % 8 == 0) ? 1 : 0;
         st = sp.NT == 2 ? launch_state<kModeMap, 2>(p, sg, sp.NW_map, stream)
                         : launch_state<kModeMap, 1>(p, sg, sp.NW_map, stream);
         if (st != GDN_OK) return st;
+        const long long nscan = nheads * (p.dv / 16);
+        if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
+        hipLaunchKernelGGL(gdn_prefill_scan_kernel, dim3(static_cast<unsigned>(nscan)), dim3(256), 0, stream, p, sg);
+        st = gdn_host::check_launch("gdn_prefill_scan_kernel");
+        if (st != GDN_OK) return st;
     }
     sg.nvg = sp.nvg_out;
+    sg.ngroups_run = sp.G;
+    sg.xcd_map = ((nheads * sp.G) % 8 == 0) ? 1 : 0;
     return sp.NT == 2 ? launch_state<kModeOut, 2>(p, sg, sp.NW_out, stream)
                       : launch_state<kModeOut, 1>(p, sg, sp.NW_out, stream);
 }
