@@ -99,11 +99,31 @@ __device__ __forceinline__ int rho_row(int r, int g, int i) { return 32 * (r >> 
 // ---------------------------------------------------------------------------
 // Kernel 1
 // ---------------------------------------------------------------------------
+// Inclusive prefix sum over the 64 lanes with DPP: shifts by 1, 2, 4, 8 within
+// each 16-lane row, then lane 15 broadcast into rows 1 and 3 and lane 31 into
+// rows 2 and 3.  Lanes without a source add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add_src(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
+}
+__device__ __forceinline__ float wave_inclusive_sum(float v) {
+    v += dpp_add_src<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_add_src<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_add_src<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_add_src<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_add_src<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp_add_src<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
 constexpr int kKLD = kDK + 8;  // padded LDS row (bf16) for K and Q tiles
-constexpr int kAQ = kC / 4 + 4;  // A stored de-interleaved: Ad[i][j % 4][j / 4], padded
+constexpr int kAQ = kC / 4 + 4;  // A stored by column, de-interleaved: Ad[j][i % 4][i / 4], padded
 constexpr int kBLD = kC + 8;   // padded LDS row (bf16) for 64x64 tiles
 
-__global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p) {
+// LDS use (about 73 KiB) allows two workgroups per CU, i.e. two waves per
+// SIMD: saying so lets the scheduler spend registers on hoisting LDS loads.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gdn_prefill_intra_kernel(
+    PrefillParams p) {
     const int c = blockIdx.x;
     const int h = blockIdx.y;
     const int sidx = blockIdx.z;
@@ -126,6 +146,17 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
     __shared__ __attribute__((aligned(16))) bf16 Tl[kC][kBLD];
     __shared__ float s_lgc[kC], s_bm[kC], s_ms[kC], s_kdec[kC];
 
+    // Gate inputs (wave 0, one token per lane) are read first so their
+    // latency overlaps the K/Q tile loads.
+    const bool tok_ok = wave == 0 && lane < nvalid;
+    float g_m = 0.f, g_a = 0.f, g_b = 0.f;
+    if (tok_ok) {
+        const size_t gi = row_base + lane;
+        g_m = p.mask ? p.mask[static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + t0 + lane] : 1.f;
+        g_a = bf2f(p.a[gi]);
+        g_b = bf2f(p.b[gi]);
+    }
+
     // 1) K and Q tiles into LDS; rows past the sequence end are zero.
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -145,19 +176,13 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
     if (wave == 0) {
         const int t = lane;
         float lg = 0.f, bm = 0.f, m = 0.f;
-        if (t < nvalid) {
-            const size_t gi = row_base + t;
-            m = p.mask ? p.mask[static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + t0 + t] : 1.f;
-            lg = -expf(p.A_log[h]) * softplus_f(bf2f(p.a[gi]) + p.dt_bias);
-            bm = sigmoid_f(bf2f(p.b[gi])) * m;
+        if (tok_ok) {
+            m = g_m;
+            lg = -expf(p.A_log[h]) * softplus_f(g_a + p.dt_bias);
+            bm = sigmoid_f(g_b) * m;
         }
-        float s = lg;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const float u = __shfl_up(s, off);
-            if (lane >= off) s += u;
-        }
-        const float last = __shfl(s, kWave - 1);
+        const float s = wave_inclusive_sum(lg);
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), kWave - 1));
         s_lgc[t] = s;
         s_bm[t] = bm;
         s_ms[t] = m * p.scale;
@@ -197,7 +222,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * ti + 4 * g4 + i;
             const float d = expf(s_lgc[row] - lgc_col);
-            Ad[row][col & 3][col >> 2] = row > col ? s_bm[row] * accK[i] * d : 0.f;
+            Ad[col][row & 3][row >> 2] = row > col ? s_bm[row] * accK[i] * d : 0.f;
             Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
         }
     }
@@ -228,37 +253,53 @@ __global__ __launch_bounds__(256) void gdn_prefill_intra_kernel(PrefillParams p)
         }
     }
 
-    // 5) T = (I + A)^-1 by forward substitution, fp32, on all 4 waves: column
-    //    c = 16 wave + lane/4 is owned by a quad; lane sub = lane % 4 keeps
-    //    rows j = 4q + sub of it (Tc[q]) and sums A[i][j] T[j][c] over its j;
-    //    two DPP quad adds give the row's total.
+    // 5) T = (I + A)^-1 by forward substitution, fp32, on all 4 waves,
+    //    right-looking: column c = 16 wave + lane/4 is owned by a quad; lane
+    //    sub = lane % 4 keeps rows i = 4q + sub (Tc[q]) and their running sums
+    //    acc[q] = sum_{j done} A[i][j] T[j][c].  Row j is final once row j-1
+    //    is folded in; its owner lane computes it, a DPP broadcast hands it to
+    //    the quad, and every lane folds it into its later rows (independent
+    //    FMAs, off the row-to-row chain).
     {
         const int c = 16 * wave + (lane >> 2);
         const int sub = lane & 3;
-        float Tc[16];
+        float Tc[16], acc[16];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) Tc[q] = 0.f;
+        for (int q = 0; q < 16; ++q) Tc[q] = acc[q] = 0.f;
+        // Row j of A (this lane's slots) is loaded two rows ahead into a
+        // ring; the empty asm keeps the scheduler from sinking the loads back
+        // to their use, so LDS latency overlaps the previous rows' chain.
+        f32x4 ring[3][4];
+        auto load_row = [&](int j, f32x4 (&dst)[4]) {
+#pragma clang loop unroll(full)
+            for (int q4 = (j >> 2) >> 2; q4 < 4; ++q4) dst[q4] = *reinterpret_cast<const f32x4*>(&Ad[j][sub][4 * q4]);
+        };
+        load_row(0, ring[0]);
+        load_row(1, ring[1]);
         // Fully unrolled (the row index must be a constant: Tc stays in registers).
 #pragma clang loop unroll(full)
-        for (int i = 0; i < kC; ++i) {
-            float part = 0.f;
-            const int nq = (i + 3) / 4;  // groups touched: q < nq
+        for (int j = 0; j < kC; ++j) {
+            if (j + 2 < kC) load_row(j + 2, ring[(j + 2) % 3]);
+            asm volatile("" ::: "memory");
+            const int qj = j >> 2, sj = j & 3;
+            const float own = (j == c ? 1.f : 0.f) - acc[qj];  // row j, valid in lane sub == sj
+            float tj;
+            if (sj == 0) tj = dpp_f<0x00>(own);       // quad_perm [0,0,0,0]
+            else if (sj == 1) tj = dpp_f<0x55>(own);  // quad_perm [1,1,1,1]
+            else if (sj == 2) tj = dpp_f<0xAA>(own);  // quad_perm [2,2,2,2]
+            else tj = dpp_f<0xFF>(own);               // quad_perm [3,3,3,3]
+            Tc[qj] = sub == sj ? tj : Tc[qj];
+            // Fold row j into rows i > j: slots q >= qj (slot qj only for sub > sj).
+            const f32x4(&a)[4] = ring[j % 3];
 #pragma clang loop unroll(full)
-            for (int q4 = 0; q4 < (nq + 3) / 4; ++q4) {
-                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ad[i][sub][4 * q4]);
+            for (int q4 = qj >> 2; q4 < 4; ++q4) {
 #pragma clang loop unroll(full)
                 for (int u = 0; u < 4; ++u) {
                     const int q = 4 * q4 + u;
-                    if (q < i / 4)
-                        part += a4[u] * Tc[q];
-                    else if (q == i / 4 && (i & 3) != 0)
-                        part += (sub < (i & 3) ? a4[u] : 0.f) * Tc[q];
+                    if (q > qj) acc[q] += a[q4][u] * tj;
+                    else if (q == qj && sj < 3) acc[q] += (sub > sj ? a[q4][u] : 0.f) * tj;
                 }
             }
-            part += dpp_f<0xB1>(part);  // quad_perm [1,0,3,2]
-            part += dpp_f<0x4E>(part);  // quad_perm [2,3,0,1]
-            const float val = (i == c ? 1.f : 0.f) - part;
-            if (sub == (i & 3)) Tc[i >> 2] = val;
         }
         const float bmc = s_bm[c];
 #pragma unroll
@@ -352,67 +393,79 @@ struct StageLane {
     uint32_t v;   // V tile: row lane / (2 NT), 8 columns (lane % (2 NT))
 };
 
-// Stage chunk operands into `buf`.  Full chunks use uniform bases plus the
-// lane offsets; the last, partial chunk clamps rows to the sequence (so no
-// load leaves the tensors) and its padded rows are zeroed after arrival.
-// Shared jobs are dealt round robin to the NW waves; each wave copies its own
-// V tile when `stage_v`.
+// Copies of one chunk's operands into `buf`, all issued together at the start
+// of the previous chunk's work (spreading them between its MFMA phases was
+// measured slower: a copy that meets a full memory pipeline stalls the MFMA
+// work queued behind it).  Shared jobs (K, Q, Tp, Aq and Kt fragments, the
+// gate block) are dealt round robin to the NW waves; each wave copies its own
+// V tile when `v_on`.  Full chunks use uniform bases plus the lane offsets;
+// the last, partial chunk clamps rows to the sequence (so no load leaves the
+// tensors) and its padded rows are zeroed after arrival.
+
 template <int MODE, int NW, int NT>
-__device__ __forceinline__ void stage_chunk(const PrefillParams& p, lds_u8* buf, size_t row_base, int nvalid,
-                                            size_t wc, int wave, int lane, int col0_wave, bool stage_v,
-                                            const StageLane& L) {
+struct Stager {
     using St = Stage<MODE, NW, NT>;
-    const unsigned char* tb = reinterpret_cast<const unsigned char*>(p.wsT + wc * 8 * 64);
-    const unsigned char* ab = reinterpret_cast<const unsigned char*>(p.wsA + wc * 8 * 64);
-    const unsigned char* ktb = reinterpret_cast<const unsigned char*>(p.wsK + wc * 16 * 64);
-    const unsigned char* gb = reinterpret_cast<const unsigned char*>(p.wsG + wc * 128);
-    constexpr int kRowsPerV = 32 / NT;  // V rows per 1 KiB copy
-    if (nvalid == kC) {
-        const unsigned char* kb = reinterpret_cast<const unsigned char*>(p.k + row_base * kDK);
-        const unsigned char* qb = reinterpret_cast<const unsigned char*>(p.q + row_base * kDK);
-#pragma unroll
-        for (int f = 0; f < 16; ++f) {
-            const uint32_t o = L.kq + (f >> 2) * 16 * kDK * 2 + (f & 3) * 64;
-            if (f % NW == wave) dma16(kb + o, buf + St::offK + f * kFragB);
-            if (St::out && (f + 16) % NW == wave) dma16(qb + o, buf + St::offQ + f * kFragB);
-        }
-        if (stage_v) {
-#pragma unroll
-            for (int it = 0; it < 2 * NT; ++it)
-                dma16(reinterpret_cast<const unsigned char*>(p.v + (row_base + kRowsPerV * it) * p.dv) + L.v,
-                      buf + St::offV + wave * St::vWave + it * kFragB);
-        }
-    } else {
+    static constexpr int nK = 16, nQ = St::out ? 16 : 0, nT = 8, nA = St::out ? 6 : 0, nKt = 16;
+    static constexpr int NJ = nK + nQ + nT + nA + nKt + 1;  // + the gate block
+    const PrefillParams* p;
+    lds_u8* buf;
+    size_t row_base, wc;
+    int nvalid, wave, lane, col0_wave;
+    bool on, v_on;
+    const StageLane* L;
+
+    __device__ __forceinline__ void issue() const {
+        if (!on) return;
+        const bool full = nvalid == kC;
         const int m = lane & 15, g = lane >> 4;
 #pragma unroll
-        for (int f = 0; f < 16; ++f) {
-            const int row = min(16 * (f >> 2) + m, nvalid - 1);
-            const size_t e = (row_base + row) * kDK + 32 * (f & 3) + 8 * g;
-            if (f % NW == wave) dma16(p.k + e, buf + St::offK + f * kFragB);
-            if (St::out && (f + 16) % NW == wave) dma16(p.q + e, buf + St::offQ + f * kFragB);
+        for (int f = 0; f < NJ; ++f) {
+            if (f % NW != wave) continue;  // uniform
+            if (f < nK + nQ) {
+                const bool isq = f >= nK;
+                const int ff = isq ? f - nK : f;
+                const uint16_t* base = isq ? p->q : p->k;
+                const void* src;
+                if (full) {
+                    src = reinterpret_cast<const unsigned char*>(base + row_base * kDK) + L->kq +
+                          (ff >> 2) * 16 * kDK * 2 + (ff & 3) * 64;
+                } else {
+                    const int row = min(16 * (ff >> 2) + m, nvalid - 1);
+                    src = base + (row_base + row) * kDK + 32 * (ff & 3) + 8 * g;
+                }
+                dma16(src, buf + (isq ? St::offQ : St::offK) + ff * kFragB);
+            } else if (f < nK + nQ + nT) {
+                const int ff = f - nK - nQ;
+                dma16(reinterpret_cast<const unsigned char*>(p->wsT + wc * 8 * 64) + ff * kFragB + L->fr,
+                      buf + St::offT + ff * kFragB);
+            } else if (f < nK + nQ + nT + nA) {
+                const int ff = f - nK - nQ - nT;
+                dma16(reinterpret_cast<const unsigned char*>(p->wsA + wc * 8 * 64) + aq_slot(ff) * kFragB + L->fr,
+                      buf + St::offA + ff * kFragB);
+            } else if (f < NJ - 1) {
+                const int ff = f - nK - nQ - nT - nA;
+                dma16(reinterpret_cast<const unsigned char*>(p->wsK + wc * 16 * 64) + ff * kFragB + L->fr,
+                      buf + St::offKt + ff * kFragB);
+            } else {
+                dma16(reinterpret_cast<const unsigned char*>(p->wsG + wc * 128) + L->g, buf + St::offG);
+            }
         }
-        if (stage_v) {
+        if (v_on) {
+            constexpr int kRowsPerV = 32 / NT;  // V rows per 1 KiB copy
 #pragma unroll
             for (int it = 0; it < 2 * NT; ++it) {
-                const int row = min(kRowsPerV * it + lane / (2 * NT), nvalid - 1);
-                dma16(p.v + (row_base + row) * p.dv + col0_wave + 8 * (lane % (2 * NT)),
-                      buf + St::offV + wave * St::vWave + it * kFragB);
+                const void* src;
+                if (full) {
+                    src = reinterpret_cast<const unsigned char*>(p->v + (row_base + kRowsPerV * it) * p->dv) + L->v;
+                } else {
+                    const int row = min(kRowsPerV * it + lane / (2 * NT), nvalid - 1);
+                    src = p->v + (row_base + row) * p->dv + col0_wave + 8 * (lane % (2 * NT));
+                }
+                dma16(src, buf + St::offV + wave * St::vWave + it * kFragB);
             }
         }
     }
-#pragma unroll
-    for (int f = 0; f < 8; ++f)
-        if ((f + 32) % NW == wave) dma16(tb + f * kFragB + L.fr, buf + St::offT + f * kFragB);
-    if (St::out) {
-#pragma unroll
-        for (int i = 0; i < 6; ++i)
-            if ((i + 40) % NW == wave) dma16(ab + aq_slot(i) * kFragB + L.fr, buf + St::offA + i * kFragB);
-    }
-#pragma unroll
-    for (int f = 0; f < 16; ++f)
-        if ((f + 48) % NW == wave) dma16(ktb + f * kFragB + L.fr, buf + St::offKt + f * kFragB);
-    if (64 % NW == wave) dma16(gb + L.g, buf + St::offG);
-}
+};
 
 // Zero the rows >= nvalid of the staged K, Q and V (partial chunk only).
 template <int MODE, int NW, int NT>
@@ -446,30 +499,59 @@ __device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const
 }
 
 // One chunk of the state recurrence for a 128 x (16 NT) column tile, operands
-// in LDS.  `ob` points at out[row_base][0] (uniform).  All operand fragments
-// are read from LDS up front (none depends on the state), so the MFMA chain
-// that does depend on it never waits on LDS in between.  `v_zero`: the tile
-// has no V (identity columns of the map pass).
+// in LDS.  `ob` points at out[row_base][0] (uniform).  Operand fragments are
+// read from LDS one phase ahead of their use (none depends on the state), so
+// the MFMA chain that does depend on it rarely waits on LDS, without holding
+// every fragment in registers at once.  `v_zero`: the tile has no V (identity
+// columns of the map pass).  `next` issues the following chunk's copies.
 template <int MODE, int NW, int NT>
 __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
-                                            int wave, int lane, int col0_wave, bool v_zero) {
+                                            int wave, int lane, int col0_wave, bool v_zero,
+                                            const Stager<MODE, NW, NT>& next) {
     using St = Stage<MODE, NW, NT>;
     const int n = lane & 15, g = lane >> 4;
     const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + St::offG);
     const lds_u16* Vs = reinterpret_cast<const lds_u16*>(buf + St::offV + wave * St::vWave);
 
-    bf16x8 kf[16], qf[St::out ? 16 : 1], tf[8], af[St::out ? 6 : 1], ktf[16];
+    next.issue();
+
+    // (a) X = K S (and P = Q S for the output), in two k-halves so only half
+    //     of the K and Q fragments is held at a time.
+    f32x4 X[4][NT], P[4][NT];
 #pragma unroll
-    for (int f = 0; f < 16; ++f) {
-        kf[f] = frag(buf, St::offK + f * kFragB, lane);
-        if constexpr (St::out) qf[f] = frag(buf, St::offQ + f * kFragB, lane);
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        bf16x8 kf[4][2], qf[St::out ? 4 : 1][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int f = 4 * mt + 2 * half + s2;
+                kf[mt][s2] = frag(buf, St::offK + f * kFragB, lane);
+                if constexpr (St::out) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
+            }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int s = 2 * half + s2;
+            bf16x8 Bs[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    X[mt][nt] = mfma16x16x32(kf[mt][s2], Bs[nt], X[mt][nt]);
+                    if constexpr (St::out) P[mt][nt] = mfma16x16x32(qf[mt][s2], Bs[nt], P[mt][nt]);
+                }
+        }
     }
+    bf16x8 tf[8], af[St::out ? 6 : 1], ktf[16];
+    // Tp and Kt for (c) and (e), read while (a) drains.
 #pragma unroll
     for (int f = 0; f < 8; ++f) tf[f] = frag(buf, St::offT + f * kFragB, lane);
-    if constexpr (St::out) {
-#pragma unroll
-        for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offA + i * kFragB, lane);
-    }
 #pragma unroll
     for (int f = 0; f < 16; ++f) ktf[f] = frag(buf, St::offKt + f * kFragB, lane);
     float vv[NT][16];
@@ -480,33 +562,10 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 vv[nt][4 * mt + i] = v_zero ? 0.f : bf2f(Vs[(16 * mt + 4 * g + i) * 16 * NT + 16 * nt + n]);
-    f32x4 gam[4], co[4];
+    f32x4 gam[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
-        if constexpr (St::out) co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
-    }
+    for (int mt = 0; mt < 4; ++mt) gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
     const float gC = G[kC - 1];
-
-    // (a) X = K S (and P = Q S for the output).
-    f32x4 X[4][NT], P[4][NT];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        bf16x8 Bs[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                X[mt][nt] = mfma16x16x32(kf[4 * mt + s], Bs[nt], X[mt][nt]);
-                if constexpr (St::out) P[mt][nt] = mfma16x16x32(qf[4 * mt + s], Bs[nt], P[mt][nt]);
-            }
-    }
     // (b) Y = V - gamma o X (in place in X).
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -530,6 +589,10 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) D[mt][nt] = mfma16x16x32(tf[2 * mt + s], BY[nt], D[mt][nt]);
     }
+    if constexpr (St::out) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offA + i * kFragB, lane);
+    }
     bf16x8 BD0[NT], BD1[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -547,6 +610,9 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
         }
     if constexpr (!St::out) return;
     // (d) O = (m scale gamma) o P + Aq dV -> bf16.
+    f32x4 co[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         f32x4 O[4];
@@ -578,9 +644,11 @@ struct StateGrid {
     int ngroups_run; // groups per sequence this launch covers (map pass: G - 1)
     int nheads;      // sequences x heads
     int xcd_map;     // deal the workgroups of one (head, group) to one XCD
-    float* psi;      // [nheads][G][dv/16][64][32] fp32: map pass zero-state results, then
-                     // (scan) the initial state of group j + 1 in slot j
-    uint16_t* phi;   // map pass: transitions, [nheads][G][128][128] bf16 row-major
+    float* psi;      // [nheads][G][dv/16][8][64][4] fp32 (16-column tile, accumulator tile r,
+                     // lane, slot): map pass zero-state results, then (scan) the initial
+                     // state of group j + 1 in slot j
+    uint16_t* phi;   // map pass: transitions as MFMA A fragments, [nheads][G][8][4][64][8]
+                     // bf16 (row tile r, k-step, lane: row rho(r, n/4, n%4), columns 32ks + 8g..)
 };
 
 // State pass over one chunk group per workgroup (NW waves, NT 16-column tiles
@@ -646,10 +714,9 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const f32x4* Ps = reinterpret_cast<const f32x4*>(
-                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048 +
-                lane * 32);
+                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048);
 #pragma unroll
-            for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r];
+            for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r * 64 + lane];
         }
     } else if (p.state_in) {
         const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
@@ -677,20 +744,21 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
         else
             wait_vm<St::stores>();
         lds_barrier();  // chunk c staged by every wave; nobody still reads `nxt`
-        if (c + 1 < c_end)
-            stage_chunk<MODE, NW, NT>(p, nxt, rows(c + 1), nval(c + 1), wcof(c + 1), wave, lane, col0_wave,
-                                      !phi_cols, L);
+        const Stager<MODE, NW, NT> next = {&p,   nxt,  rows(c + 1), wcof(c + 1),     nval(c + 1), wave,
+                                           lane, col0_wave, c + 1 < c_end, !phi_cols, &L};
         const int nv = nval(c);
         if (nv < kC) {
             zero_pad_rows<MODE, NW, NT>(cur, nv, wave, lane);
             lds_barrier();
         }
-        state_chunk<MODE, NW, NT>(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col0_wave, phi_cols);
+        state_chunk<MODE, NW, NT>(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col0_wave, phi_cols, next);
     };
 
-    if (c_begin < c_end)
-        stage_chunk<MODE, NW, NT>(p, buf0, rows(c_begin), nval(c_begin), wcof(c_begin), wave, lane, col0_wave,
-                                  !phi_cols, L);
+    {
+        const Stager<MODE, NW, NT> first = {&p,   buf0, rows(c_begin), wcof(c_begin),   nval(c_begin), wave,
+                                            lane, col0_wave, c_begin < c_end, !phi_cols, &L};
+        first.issue();
+    }
     for (int c = c_begin; c < c_end; c += 2) {
         step(c, buf0, buf1);
         if (c + 1 < c_end) step(c + 1, buf1, buf0);
@@ -706,22 +774,32 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 #pragma unroll
                 for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n] = S[r][nt][i];
     } else if (phi_cols) {
+        // phi as A fragments: the accumulator holds 16-column tile T of phi
+        // (a column per lane); a fragment lane needs 8 consecutive columns of
+        // one row.  Transpose each 16x16 tile through this wave's own V area
+        // (unused by identity columns), then store 512 contiguous bytes.
         uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + grp) * kDK * kDK;
+        lds_u16* tt = reinterpret_cast<lds_u16*>(buf0 + St::offV + wave * St::vWave);
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+            for (int nt = 0; nt < NT; ++nt) {
+                const int T = (col0_wave - dv) / 16 + nt;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    Ph[rho_row(r, g, i) * kDK + col0_wave - dv + 16 * nt + n] = f2bf_bits(S[r][nt][i]);
+                for (int i = 0; i < 4; ++i) tt[(4 * g + i) * 16 + n] = f2bf_bits(S[r][nt][i]);
+                if (lane < 32) {  // fragment lanes 16 (2 (T % 2) + h) + n: row n of the tile, columns 8h..
+                    const int h = lane >> 4;
+                    const u32x4 v = *reinterpret_cast<const lds_u32x4*>(tt + n * 16 + 8 * h);
+                    *reinterpret_cast<u32x4*>(Ph + ((r * 4 + (T >> 1)) * 64 + 16 * (2 * (T & 1) + h) + n) * 8) = v;
+                }
+            }
     } else {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             f32x4* Ps = reinterpret_cast<f32x4*>(
-                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp) * (dv / 16) + col0_wave / 16 + nt) * 2048 +
-                lane * 32);
+                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp) * (dv / 16) + col0_wave / 16 + nt) * 2048);
 #pragma unroll
-            for (int r = 0; r < 8; ++r) Ps[r] = S[r][nt];
+            for (int r = 0; r < 8; ++r) Ps[r * 64 + lane] = S[r][nt];
         }
     }
 }
@@ -731,14 +809,19 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 // (sequence-head, 16-column tile); wave w owns state rows 32w .. 32w + 31 (row
 // tiles 2w and 2w + 1 of the accumulator order), which are exactly the rows of
 // MFMA k-step w, so each wave publishes its rows as that k-step's B operand
-// (bf16 high and low halves of the fp32 state) and reads all four back.  The
-// transitions and zero-state results of step j + 1 are loaded during step j.
+// (bf16 high and low halves of the fp32 state) and reads all four back.  Each
+// wave copies its own rows of phi_j and psi_j into an LDS ring kScanRing - 1
+// steps ahead (asynchronous copies, waited for with explicit counts).
+constexpr int kScanRing = 3;
+constexpr int kScanSlot = 10 * kFragB;  // per wave and step: 8 phi fragments, 2 psi quads
+
 __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(PrefillParams p, StateGrid sg) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][8 * kFragB];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * 8 * kFragB + kScanRing * 4 * kScanSlot];
     const int dv = p.dv, ntile = dv / 16;
     const int nunits = sg.nheads * ntile;
+    const int steps = sg.ngroups - 1;
     int u = blockIdx.x;
-    if (u >= nunits) return;
+    if (u >= nunits || steps <= 0) return;  // uniform over the workgroup
     if (nunits % 8 == 0) u = (u & 7) * (nunits >> 3) + (u >> 3);  // one head's tiles on one XCD
     const int head = u / ntile, tile = u % ntile;
     const int sidx = head / p.H, h = head % p.H;
@@ -746,6 +829,8 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(PrefillParams p, 
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
     const int col = 16 * tile + n;
+    lds_u8* const sbuf = (lds_u8*)&smem[0];
+    lds_u8* const ring = (lds_u8*)&smem[2 * 8 * kFragB] + wave * kScanSlot;
 
     f32x4 S[2];
     if (p.state_in) {
@@ -757,53 +842,58 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(PrefillParams p, 
     } else {
         S[0] = S[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const int steps = sg.ngroups - 1;
     auto psi_at = [&](int j) {
-        return reinterpret_cast<f32x4*>(sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048 +
-                                        lane * 32) + 2 * wave;
+        return sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048;
     };
-    auto load = [&](int j, bf16x8 (&A)[2][4], f32x4 (&Y)[2]) {
-        const uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK;
+    // This wave's phi fragments (row tiles 2w, 2w + 1: 8 contiguous KiB) and
+    // psi quads (2 contiguous KiB); every copy reads 1 KiB, 16 bytes a lane.
+    auto stage = [&](int j, int slot) {  // 10 copies per wave
+        const unsigned char* ph = reinterpret_cast<const unsigned char*>(
+            sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) + 8 * wave * kFragB + 16 * lane;
+        const unsigned char* ps = reinterpret_cast<const unsigned char*>(psi_at(j)) + 2 * wave * kFragB + 16 * lane;
+        lds_u8* dst = ring + slot * 4 * kScanSlot;
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                A[rr][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(
-                    Ph + rho_row(2 * wave + rr, n >> 2, n & 3) * kDK + 32 * ks + 8 * g));
-            Y[rr] = psi_at(j)[rr];
-        }
+        for (int f = 0; f < 8; ++f) dma16(ph + f * kFragB, dst + f * kFragB);  // (rr, ks) = (f / 4, f % 4)
+        dma16(ps, dst + 8 * kFragB);
+        dma16(ps + kFragB, dst + 9 * kFragB);
     };
-    auto step = [&](int j, lds_u8* buf, const bf16x8 (&A)[2][4], const f32x4 (&Y)[2], bf16x8 (&An)[2][4],
-                    f32x4 (&Yn)[2]) {
+    // Every step issues one stage (clamped to the last step), so the copy for
+    // step j always has exactly 2 (stores) + 10 + 2 operations after it when
+    // step j begins, for kScanRing = 3.
+    static_assert(kScanRing == 3, "wait count below assumes a 3-deep ring");
+#pragma unroll
+    for (int d = 0; d < kScanRing - 1; ++d) stage(min(d, steps - 1), d);
+    for (int j = 0; j < steps; ++j) {
+        const int slot = j % kScanRing;
+        lds_u8* const buf = sbuf + (j & 1) * 8 * kFragB;
         const bf16x8 hi = pack8(S[0], S[1]);
         *reinterpret_cast<lds_bf16x8*>(buf + (2 * wave) * kFragB + 16 * lane) = hi;
         *reinterpret_cast<lds_bf16x8*>(buf + (2 * wave + 1) * kFragB + 16 * lane) = pack8_lo(S[0], S[1], hi);
+        if (j == 0)
+            wait_vm<10>();  // the first stage; the second may still be in flight
+        else
+            wait_vm<14>();
         lds_barrier();
-        if (j + 1 < steps) load(j + 1, An, Yn);
-        f32x4 acc[2] = {Y[0], Y[1]};
+        stage(min(j + kScanRing - 1, steps - 1), (j + kScanRing - 1) % kScanRing);
+        const lds_u8* src = ring + slot * 4 * kScanSlot;
+        f32x4 acc[2] = {*reinterpret_cast<const lds_f32x4*>(src + 8 * kFragB + 16 * lane),
+                        *reinterpret_cast<const lds_f32x4*>(src + 9 * kFragB + 16 * lane)};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const bf16x8 bh = frag(buf, (2 * ks) * kFragB, lane);
             const bf16x8 bl = frag(buf, (2 * ks + 1) * kFragB, lane);
 #pragma unroll
             for (int rr = 0; rr < 2; ++rr) {
-                acc[rr] = mfma16x16x32(A[rr][ks], bh, acc[rr]);
-                acc[rr] = mfma16x16x32(A[rr][ks], bl, acc[rr]);
+                const bf16x8 a = frag(src, (4 * rr + ks) * kFragB, lane);
+                acc[rr] = mfma16x16x32(a, bh, acc[rr]);
+                acc[rr] = mfma16x16x32(a, bl, acc[rr]);
             }
         }
-        f32x4* out = psi_at(j);
+        f32x4* out = reinterpret_cast<f32x4*>(psi_at(j)) + 2 * wave * 64 + lane;
         out[0] = S[0] = acc[0];
-        out[1] = S[1] = acc[1];
-    };
-    bf16x8 A0[2][4], A1[2][4];
-    f32x4 Y0[2], Y1[2];
-    if (steps > 0) load(0, A0, Y0);
-    lds_u8* const buf0 = (lds_u8*)&smem[0][0];
-    lds_u8* const buf1 = (lds_u8*)&smem[1][0];
-    for (int j = 0; j < steps; j += 2) {
-        step(j, buf0, A0, Y0, A1, Y1);
-        if (j + 1 < steps) step(j + 1, buf1, A1, Y1, A0, Y0);
+        out[64] = S[1] = acc[1];
     }
+    wait_vm<0>();  // the clamped trailing copies land before the workgroup's LDS is released
 }
 
 // ---------------------------------------------------------------------------
