@@ -15,9 +15,11 @@
 // per chunk (bf16 unless noted), already in the register order the state
 // kernels' MFMA operands need (one 16-byte load per lane per fragment):
 //   Tp  = T diag(beta m)                       8 fragments  (8 KiB)
-//   Aq  = m scale (Q K^T o Gamma), t >= s      8 fragments  (8 KiB)
-//   Kt  = (K o gamma_C/gamma)^T                16 fragments (16 KiB)
-//   G   = [gamma_t, m_t scale gamma_t]         128 fp32
+//   Aq  = m scale (Q K^T o Gamma), t >= s      the 6 nonzero fragments (6 KiB)
+//   G   = [gamma_t, m_t scale gamma_t, gamma_C / gamma_t, -]   256 fp32
+// The state update's K^T operand is not stored: the state kernels build it
+// from the K tile they stage anyway, with transposing LDS reads, and apply
+// gamma_C / gamma_t to the rows of dV instead.
 // Kernel 2, gdn_prefill_state_kernel — each wave owns 16*NT state columns of
 // one (sequence, head) and walks chunks in order.  The fp32 state tile lives
 // in MFMA accumulator registers the whole time; its bf16 copy feeds the next
@@ -60,7 +62,6 @@ struct PrefillParams {
     const int32_t* cu;  // varlen offsets (nullable: batch mode)
     u32x4* wsT;
     u32x4* wsA;
-    u32x4* wsK;
     float* wsG;
     float dt_bias;
     float scale;
@@ -95,6 +96,10 @@ __device__ __forceinline__ SeqInfo seq_info(const PrefillParams& p, int sidx) {
 
 __device__ __forceinline__ int pi_pos(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4); }
 __device__ __forceinline__ int rho_row(int r, int g, int i) { return 32 * (r >> 1) + 8 * g + 4 * (r & 1) + i; }
+
+// The nonzero fragments (mt, s) of the causal Aq, in workspace order:
+// (0,0),(1,0),(2,0),(2,1),(3,0),(3,1) as f = 2 mt + s.
+__device__ __forceinline__ constexpr int aq_slot(int i) { return i < 2 ? 2 * i : i + 2; }
 
 // ---------------------------------------------------------------------------
 // Kernel 1
@@ -144,7 +149,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     __shared__ __attribute__((aligned(16))) float Ad[kC][4][kAQ];
     __shared__ __attribute__((aligned(16))) bf16 Al[kC][kBLD];
     __shared__ __attribute__((aligned(16))) bf16 Tl[kC][kBLD];
-    __shared__ float s_lgc[kC], s_bm[kC], s_ms[kC], s_kdec[kC];
+    __shared__ float s_lgc[kC], s_bm[kC], s_ms[kC];
 
     // Gate inputs (wave 0, one token per lane) are read first so their
     // latency overlaps the K/Q tile loads.
@@ -186,11 +191,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         s_lgc[t] = s;
         s_bm[t] = bm;
         s_ms[t] = m * p.scale;
-        s_kdec[t] = expf(last - s);
         const float gam = expf(s);
-        float* G = p.wsG + wc * 128;
+        float* G = p.wsG + wc * 256;
         G[t] = gam;
         G[64 + t] = m * p.scale * gam;
+        G[128 + t] = expf(last - s);
     }
     __syncthreads();
 
@@ -228,29 +233,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
     __syncthreads();
 
-    // 4) Aq fragments (8) and Kt fragments (16), six per wave.
-    //    Aq (mt, s): lane holds Aq[16mt + m][32s + pi(g, j)].
-    //    Kt (r, s):  lane holds K[32s + pi(g,j)][rho(r, m/4, m%4)] * gamma_C / gamma_t.
+    // 4) The six nonzero Aq fragments (mt, s) = (0,0),(1,0),(2,0),(2,1),(3,0),(3,1):
+    //    lane holds Aq[16mt + m][32s + pi(g, j)].
 #pragma unroll
-    for (int f = 0; f < 24; ++f) {
-        if (f % 4 != wave) continue;
-        if (f < 8) {
-            const int mt = f >> 1, s = f & 1;
-            const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
-            p.wsA[(wc * 8 + f) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        } else {
-            const int fk = f - 8, r = fk >> 1, s = fk & 1;
-            const int krow = rho_row(r, m16 >> 2, m16 & 3);
-            bf16x8 fr;
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const int t = 32 * s + pi_pos(g4, jj);
-                fr[jj] = f2bf(bf2f(Kl[t][krow]) * s_kdec[t]);
-            }
-            p.wsK[(wc * 16 + fk) * 64 + lane] = __builtin_bit_cast(u32x4, fr);
-        }
+    for (int i = 0; i < 6; ++i) {
+        if (i % 4 != wave) continue;
+        const int f = aq_slot(i), mt = f >> 1, s = f & 1;
+        const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
+        p.wsA[(wc * 6 + i) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
 
     // 5) T = (I + A)^-1 by forward substitution, fp32, on all 4 waves,
@@ -332,20 +324,17 @@ enum { kModeOut = 0, kModeMap = 1 };
 template <int MODE, int NW, int NT>
 struct Stage {
     static constexpr bool out = MODE == kModeOut;
-    static constexpr int offK = 0;                                  // 16: (mt, s) -> K rows 16mt+m, k 32s+8g
+    static constexpr int offK = 0;                                  // 16: (mt, s), lane slots swizzled (kslot)
     static constexpr int offQ = offK + 16 * kFragB;                 // 16 (out only)
     static constexpr int offT = offQ + (out ? 16 : 0) * kFragB;     // 8: Tp (mt, s)
     static constexpr int offA = offT + 8 * kFragB;                  // 6 (out only): Aq slots used
-    static constexpr int offKt = offA + (out ? 6 : 0) * kFragB;     // 16: Kt (r, s)
-    static constexpr int offG = offKt + 16 * kFragB;                // gamma[64], m scale gamma[64]
+    static constexpr int offG = offA + (out ? 6 : 0) * kFragB;      // gamma, m scale gamma, gamma_C/gamma
     static constexpr int offV = offG + kFragB;
     static constexpr int vWave = 2 * NT * kFragB;
     static constexpr int bytes = offV + NW * vWave;
-    static constexpr int stores = out ? 16 * NT : 0;                // output stores per chunk per wave
+    static constexpr int stores = out ? 2 * NT : 0;                 // output stores per chunk per wave
 };
 
-// Aq workspace fragments (mt, s) read by the output: (0,0),(1,0),(2,0),(2,1),(3,0),(3,1).
-__device__ __forceinline__ constexpr int aq_slot(int i) { return i < 2 ? 2 * i : i + 2; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -355,18 +344,21 @@ typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 typedef __attribute__((address_space(3))) float lds_f32;
 typedef __attribute__((address_space(3))) uint16_t lds_u16;
 
-// 16 bytes per lane from g (per-lane address) to lds_base + 16 lane; lds_base
-// must be uniform over the wave.  Asynchronous: completion is vmcnt.  Issued
-// as inline asm so the compiler's wait-count pass does not drain the copy
-// before unrelated LDS reads of the other buffer (it cannot prove they do not
-// alias); the kernels order copies with their own vmcnt waits and barriers.
-// M0 is otherwise unused on gfx950 (LDS instructions do not read it), so the
-// clobber is safe here.
+// 16 bytes per lane from sbase + voff (sbase uniform over the wave, voff the
+// lane's 32-bit byte offset) to lds_base + 16 lane (lds_base uniform).
+// Asynchronous: completion is vmcnt.  The scalar-base form keeps source
+// addresses to one 32-bit register per lane: 64-bit per-lane pointers spill
+// in the state kernels, and a spill reload between copies makes the compiler
+// wait for every copy issued before it.  Issued as inline asm so the
+// compiler's wait-count pass does not drain the copy before unrelated LDS
+// reads of the other buffer (it cannot prove they do not alias); the kernels
+// order copies with their own vmcnt waits and barriers.  M0 is otherwise
+// unused on gfx950 (LDS instructions do not read it), so the clobber is safe.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* g, lds_u8* lds_base) {
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, lds_u8* lds_base) {
     const uint32_t m0v = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0v), "v"(g)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0v), "v"(voff), "s"(sbase)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -387,11 +379,19 @@ __device__ __forceinline__ void wait_vm() {
 
 // Per-lane byte offsets of the staging copies, fixed for the whole kernel.
 struct StageLane {
-    uint32_t kq;  // K/Q fragment: row (lane & 15), k offset 8 (lane >> 4)
-    uint32_t fr;  // workspace fragment: 16 lane
-    uint32_t g;   // gate block: 16 (lane & 31)
+    uint32_t k;   // K fragment slot `lane`: row kslot_row(lane), k offset 8 (lane >> 4)
+    uint32_t q;   // Q fragment: row (lane & 15), k offset 8 (lane >> 4)
+    uint32_t fr;  // workspace fragment or gate block: 16 lane
     uint32_t v;   // V tile: row lane / (2 NT), 8 columns (lane % (2 NT))
 };
+
+// K fragments are staged with their 16-byte lane slots swizzled: the data of
+// fragment lane (m, g) (row m, k group g) sits in slot 16 g + (m ^ 4 g).
+// Plain fragment reads stay conflict free, and the transposing reads that
+// build K^T (16 lanes reading rows T0..T0+3 of four k groups) hit 16
+// different slots modulo 16 instead of 4.
+__device__ __forceinline__ int kslot(int m, int g) { return 16 * g + (m ^ (4 * g)); }
+__device__ __forceinline__ int kslot_row(int slot) { return (slot & 15) ^ (4 * (slot >> 4)); }
 
 // Copies of one chunk's operands into `buf`, all issued together at the start
 // of the previous chunk's work (spreading them between its MFMA phases was
@@ -405,8 +405,8 @@ struct StageLane {
 template <int MODE, int NW, int NT>
 struct Stager {
     using St = Stage<MODE, NW, NT>;
-    static constexpr int nK = 16, nQ = St::out ? 16 : 0, nT = 8, nA = St::out ? 6 : 0, nKt = 16;
-    static constexpr int NJ = nK + nQ + nT + nA + nKt + 1;  // + the gate block
+    static constexpr int nK = 16, nQ = St::out ? 16 : 0, nT = 8, nA = St::out ? 6 : 0;
+    static constexpr int NJ = nK + nQ + nT + nA + 1;  // + the gate block
     const PrefillParams* p;
     lds_u8* buf;
     size_t row_base, wc;
@@ -418,50 +418,48 @@ struct Stager {
         if (!on) return;
         const bool full = nvalid == kC;
         const int m = lane & 15, g = lane >> 4;
+        const unsigned char* kb = reinterpret_cast<const unsigned char*>(p->k + row_base * kDK);
+        const unsigned char* qb = reinterpret_cast<const unsigned char*>(p->q + row_base * kDK);
 #pragma unroll
         for (int f = 0; f < NJ; ++f) {
             if (f % NW != wave) continue;  // uniform
             if (f < nK + nQ) {
                 const bool isq = f >= nK;
                 const int ff = isq ? f - nK : f;
-                const uint16_t* base = isq ? p->q : p->k;
-                const void* src;
+                const unsigned char* base = isq ? qb : kb;
                 if (full) {
-                    src = reinterpret_cast<const unsigned char*>(base + row_base * kDK) + L->kq +
-                          (ff >> 2) * 16 * kDK * 2 + (ff & 3) * 64;
+                    dma16(base + (ff >> 2) * 16 * kDK * 2 + (ff & 3) * 64, isq ? L->q : L->k,
+                          buf + (isq ? St::offQ : St::offK) + ff * kFragB);
                 } else {
-                    const int row = min(16 * (ff >> 2) + m, nvalid - 1);
-                    src = base + (row_base + row) * kDK + 32 * (ff & 3) + 8 * g;
+                    const int row = min(16 * (ff >> 2) + (isq ? m : kslot_row(lane)), nvalid - 1);
+                    dma16(base, static_cast<uint32_t>((row * kDK + 32 * (ff & 3) + 8 * g) * 2),
+                          buf + (isq ? St::offQ : St::offK) + ff * kFragB);
                 }
-                dma16(src, buf + (isq ? St::offQ : St::offK) + ff * kFragB);
             } else if (f < nK + nQ + nT) {
                 const int ff = f - nK - nQ;
-                dma16(reinterpret_cast<const unsigned char*>(p->wsT + wc * 8 * 64) + ff * kFragB + L->fr,
+                dma16(reinterpret_cast<const unsigned char*>(p->wsT + wc * 8 * 64) + ff * kFragB, L->fr,
                       buf + St::offT + ff * kFragB);
             } else if (f < nK + nQ + nT + nA) {
                 const int ff = f - nK - nQ - nT;
-                dma16(reinterpret_cast<const unsigned char*>(p->wsA + wc * 8 * 64) + aq_slot(ff) * kFragB + L->fr,
+                dma16(reinterpret_cast<const unsigned char*>(p->wsA + wc * 6 * 64) + ff * kFragB, L->fr,
                       buf + St::offA + ff * kFragB);
-            } else if (f < NJ - 1) {
-                const int ff = f - nK - nQ - nT - nA;
-                dma16(reinterpret_cast<const unsigned char*>(p->wsK + wc * 16 * 64) + ff * kFragB + L->fr,
-                      buf + St::offKt + ff * kFragB);
             } else {
-                dma16(reinterpret_cast<const unsigned char*>(p->wsG + wc * 128) + L->g, buf + St::offG);
+                dma16(p->wsG + wc * 256, L->fr, buf + St::offG);
             }
         }
         if (v_on) {
             constexpr int kRowsPerV = 32 / NT;  // V rows per 1 KiB copy
 #pragma unroll
             for (int it = 0; it < 2 * NT; ++it) {
-                const void* src;
                 if (full) {
-                    src = reinterpret_cast<const unsigned char*>(p->v + (row_base + kRowsPerV * it) * p->dv) + L->v;
+                    dma16(p->v + (row_base + kRowsPerV * it) * p->dv, L->v,
+                          buf + St::offV + wave * St::vWave + it * kFragB);
                 } else {
                     const int row = min(kRowsPerV * it + lane / (2 * NT), nvalid - 1);
-                    src = p->v + (row_base + row) * p->dv + col0_wave + 8 * (lane % (2 * NT));
+                    dma16(p->v + row_base * p->dv,
+                          static_cast<uint32_t>((row * p->dv + col0_wave + 8 * (lane % (2 * NT))) * 2),
+                          buf + St::offV + wave * St::vWave + it * kFragB);
                 }
-                dma16(src, buf + St::offV + wave * St::vWave + it * kFragB);
             }
         }
     }
@@ -473,9 +471,9 @@ __device__ __forceinline__ void zero_pad_rows(lds_u8* buf, int nvalid, int wave,
     using St = Stage<MODE, NW, NT>;
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int f = 0; f < (St::out ? 32 : 16); ++f)
-        if (f % NW == wave && 16 * ((f & 15) >> 2) + (lane & 15) >= nvalid)
-            *reinterpret_cast<lds_u32x4*>(buf + St::offK + f * kFragB + 16 * lane) = z;  // K then Q (contiguous)
+    for (int f = 0; f < (St::out ? 32 : 16); ++f)  // K then Q (contiguous); K slots are swizzled
+        if (f % NW == wave && 16 * ((f & 15) >> 2) + (f < 16 ? kslot_row(lane) : (lane & 15)) >= nvalid)
+            *reinterpret_cast<lds_u32x4*>(buf + St::offK + f * kFragB + 16 * lane) = z;
 #pragma unroll
     for (int it = 0; it < 2 * NT; ++it)
         if ((32 / NT) * it + lane / (2 * NT) >= nvalid)
@@ -484,6 +482,35 @@ __device__ __forceinline__ void zero_pad_rows(lds_u8* buf, int nvalid, int wave,
 
 __device__ __forceinline__ bf16x8 frag(const lds_u8* buf, int off, int lane) {
     return *reinterpret_cast<const lds_bf16x8*>(buf + off + 16 * lane);
+}
+
+// K fragment f = 4 mt + s (rows 16 mt + m, k 32 s + 8 g) from the swizzled slots.
+__device__ __forceinline__ bf16x8 kfrag(const lds_u8* kbuf, int f, int lane) {
+    return *reinterpret_cast<const lds_bf16x8*>(kbuf + f * kFragB + 16 * kslot(lane & 15, lane >> 4));
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// K^T fragment (r, s), the A operand of the state update: lane (m, g) gets
+// K[32 s + pi(g, j)][rho(r, m / 4, m % 4)] for j = 0..7, from the staged K.
+// ds_read_b64_tr_b16 hands output lane i of each 16-lane group element i % 4
+// of the 8 bytes read by lanes 4 j + i / 4 (j = 0..3); so source lane 4 j + a
+// reads row T0 + j at columns base(a) .. base(a) + 3, base(a) = rho(r, a, 0),
+// and output lane m = 4 a + p receives column rho(r, a, p) of rows T0 .. T0 + 3.
+// Two such reads (T0 = 32 s + 4 g and 32 s + 16 + 4 g) give the pi order.
+// Only the K slot depends on the lane (row 4 g + j of the 16-row block,
+// k group a): `kt_lane` = 16 kslot(4 g + j, a), computed once; the rest of
+// the address is a compile-time offset.
+__device__ __forceinline__ uint32_t kt_lane_offset(int lane) {
+    return 16u * static_cast<uint32_t>(kslot(4 * (lane >> 4) + ((lane >> 2) & 3), lane & 3));
+}
+__device__ __forceinline__ bf16x8 ktfrag(const lds_u8* kbuf, uint32_t kt_lane, int r, int s) {
+    const lds_u8* base = kbuf + kt_lane + (r >> 1) * kFragB + 8 * (r & 1);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + (2 * s) * 4 * kFragB));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + (2 * s + 1) * 4 * kFragB));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
 }
 
 // bf16 of (x - bf16(x)) for a pair of accumulator quads: the low half of a
@@ -506,7 +533,7 @@ __device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const
 // columns of the map pass).  `next` issues the following chunk's copies.
 template <int MODE, int NW, int NT>
 __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
-                                            int wave, int lane, int col0_wave, bool v_zero,
+                                            int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
                                             const Stager<MODE, NW, NT>& next) {
     using St = Stage<MODE, NW, NT>;
     const int n = lane & 15, g = lane >> 4;
@@ -530,7 +557,7 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
                 const int f = 4 * mt + 2 * half + s2;
-                kf[mt][s2] = frag(buf, St::offK + f * kFragB, lane);
+                kf[mt][s2] = kfrag(buf + St::offK, f, lane);
                 if constexpr (St::out) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
             }
 #pragma unroll
@@ -548,20 +575,34 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
                 }
         }
     }
-    bf16x8 tf[8], af[St::out ? 6 : 1], ktf[16];
+    bf16x8 tf[8], af[St::out ? 6 : 1], ktf[8][2];
     // Tp and Kt for (c) and (e), read while (a) drains.
 #pragma unroll
     for (int f = 0; f < 8; ++f) tf[f] = frag(buf, St::offT + f * kFragB, lane);
 #pragma unroll
-    for (int f = 0; f < 16; ++f) ktf[f] = frag(buf, St::offKt + f * kFragB, lane);
+    for (int r = 0; r < 8; ++r) {
+        ktf[r][0] = ktfrag(buf + St::offK, kt_lane, r, 0);
+        ktf[r][1] = ktfrag(buf + St::offK, kt_lane, r, 1);
+    }
+    // V in the accumulator layout (column n, rows 16 mt + 4 g + i): one
+    // transposing read per (mt, nt) -- source lane 4 j + a of group g reads
+    // row 16 mt + 4 g + j at columns 16 nt + 4 a .. + 3.
     float vv[NT][16];
+    const lds_u8* vrow = reinterpret_cast<const lds_u8*>(Vs) + ((4 * g + ((lane >> 2) & 3)) * 16 * NT + 4 * (lane & 3)) * 2;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt) {
+            if (v_zero) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                vv[nt][4 * mt + i] = v_zero ? 0.f : bf2f(Vs[(16 * mt + 4 * g + i) * 16 * NT + 16 * nt + n]);
+                for (int i = 0; i < 4; ++i) vv[nt][4 * mt + i] = 0.f;
+            } else {
+                const i16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4*)(vrow + (16 * mt * 16 * NT + 16 * nt) * 2));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vv[nt][4 * mt + i] = bf2f(static_cast<uint16_t>(t[i]));
+            }
+        }
     f32x4 gam[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
@@ -593,46 +634,66 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 #pragma unroll
         for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offA + i * kFragB, lane);
     }
-    bf16x8 BD0[NT], BD1[NT];
+    // The state update takes dV with its rows scaled by gamma_C / gamma_t
+    // (the decay from token t to the chunk end); the output takes dV as is.
+    f32x4 kd[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) kd[mt] = *reinterpret_cast<const lds_f32x4*>(G + 128 + 16 * mt + 4 * g);
+    bf16x8 BS0[NT], BS1[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        BD0[nt] = pack8(D[0][nt], D[1][nt]);
-        BD1[nt] = pack8(D[2][nt], D[3][nt]);
+        BS0[nt] = pack8(kd[0] * D[0][nt], kd[1] * D[1][nt]);
+        BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
     }
-    // (e) S <- gamma_C S + Kt dV  (issued before (d): it is the recurrence's critical path).
+    // (e) S <- gamma_C S + K^T (decay o dV)  (issued before (d): the recurrence's critical path).
 #pragma unroll
     for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             S[r][nt] *= gC;
-            S[r][nt] = mfma16x16x32(ktf[2 * r], BD0[nt], S[r][nt]);
-            S[r][nt] = mfma16x16x32(ktf[2 * r + 1], BD1[nt], S[r][nt]);
+            S[r][nt] = mfma16x16x32(ktf[r][0], BS0[nt], S[r][nt]);
+            S[r][nt] = mfma16x16x32(ktf[r][1], BS1[nt], S[r][nt]);
         }
-    if constexpr (!St::out) return;
-    // (d) O = (m scale gamma) o P + Aq dV -> bf16.
-    f32x4 co[4];
+    if constexpr (St::out) {
+        bf16x8 BD0[NT], BD1[NT];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
+        for (int nt = 0; nt < NT; ++nt) {
+            BD0[nt] = pack8(D[0][nt], D[1][nt]);
+            BD1[nt] = pack8(D[2][nt], D[3][nt]);
+        }
+        // (d) O = (m scale gamma) o P + Aq dV -> bf16, staged through this
+        //     wave's V area (free once V is in registers) so each row leaves
+        //     as 16-byte pieces: 2 NT stores per wave instead of 16 NT.  The
+        //     staged rows have their 16-byte pieces XOR-swizzled by row / 4 so
+        //     the 2-byte writes of the four lane groups hit different banks.
+        f32x4 co[4];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        f32x4 O[4];
-        O[0] = mfma16x16x32(af[0], BD0[nt], co[0] * P[0][nt]);
-        O[1] = mfma16x16x32(af[1], BD0[nt], co[1] * P[1][nt]);
-        O[2] = mfma16x16x32(af[3], BD1[nt], mfma16x16x32(af[2], BD0[nt], co[2] * P[2][nt]));
-        O[3] = mfma16x16x32(af[5], BD1[nt], mfma16x16x32(af[4], BD0[nt], co[3] * P[3][nt]));
-        const int col = col0_wave + 16 * nt + n;
+        for (int mt = 0; mt < 4; ++mt) co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
+        constexpr int kRowB = 32 * NT;          // staged row: 16 NT bf16
+        constexpr int kPieces = 2 * NT;         // 16-byte pieces per row
+        lds_u8* ot = const_cast<lds_u8*>(buf) + St::offV + wave * St::vWave;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            if (nvalid == kC) {
+        for (int nt = 0; nt < NT; ++nt) {
+            f32x4 O[4];
+            O[0] = mfma16x16x32(af[0], BD0[nt], co[0] * P[0][nt]);
+            O[1] = mfma16x16x32(af[1], BD0[nt], co[1] * P[1][nt]);
+            O[2] = mfma16x16x32(af[3], BD1[nt], mfma16x16x32(af[2], BD0[nt], co[2] * P[2][nt]));
+            O[3] = mfma16x16x32(af[5], BD1[nt], mfma16x16x32(af[4], BD0[nt], co[3] * P[3][nt]));
+            const int col = 16 * nt + n;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ob[(16 * mt + 4 * g + i) * dv + col] = f2bf_bits(O[mt][i]);
-            } else {
+            for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int row = 16 * mt + 4 * g + i;
-                    if (row < nvalid) ob[row * dv + col] = f2bf_bits(O[mt][i]);
+                    const int piece = (col >> 3) ^ ((row >> 2) & (kPieces - 1));
+                    *reinterpret_cast<lds_u16*>(ot + row * kRowB + piece * 16 + (col & 7) * 2) = f2bf_bits(O[mt][i]);
                 }
-            }
+        }
+#pragma unroll
+        for (int k = 0; k < kPieces; ++k) {
+            const int idx = 64 * k + lane, row = idx / kPieces, q = idx % kPieces;
+            const u32x4 v = *reinterpret_cast<const lds_u32x4*>(ot + row * kRowB + (q ^ ((row >> 2) & (kPieces - 1))) * 16);
+            if (row < nvalid) *reinterpret_cast<u32x4*>(ob + row * dv + col0_wave + 8 * q) = v;
         }
     }
 }
@@ -694,10 +755,13 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
     const int nchunks = (sq.len + kC - 1) / kC;
     const int glen = (nchunks + sg.ngroups - 1) / sg.ngroups;
     const int c_begin = min(grp * glen, nchunks), c_end = min(c_begin + glen, nchunks);
-    const StageLane L = {static_cast<uint32_t>((lane & 15) * kDK * 2 + (lane >> 4) * 16),
-                         static_cast<uint32_t>(16 * lane), static_cast<uint32_t>(16 * (lane & 31)),
+    const StageLane L = {static_cast<uint32_t>(kslot_row(lane) * kDK * 2 + (lane >> 4) * 16),
+                         static_cast<uint32_t>((lane & 15) * kDK * 2 + (lane >> 4) * 16),
+                         static_cast<uint32_t>(16 * lane),
                          static_cast<uint32_t>((lane / (2 * NT)) * dv * 2 + (lane % (2 * NT)) * 16 +
                                                (phi_cols ? 0 : col0_wave) * 2)};
+
+    const uint32_t kt_lane = kt_lane_offset(lane);
 
     // State tile: S[r][nt][i] = S[rho(r, g, i)][col0_wave + 16 nt + n].
     f32x4 S[8][NT];
@@ -751,7 +815,8 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
             zero_pad_rows<MODE, NW, NT>(cur, nv, wave, lane);
             lds_barrier();
         }
-        state_chunk<MODE, NW, NT>(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col0_wave, phi_cols, next);
+        state_chunk<MODE, NW, NT>(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col0_wave, phi_cols, kt_lane,
+                                  next);
     };
 
     {
@@ -847,15 +912,16 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(PrefillParams p, 
     };
     // This wave's phi fragments (row tiles 2w, 2w + 1: 8 contiguous KiB) and
     // psi quads (2 contiguous KiB); every copy reads 1 KiB, 16 bytes a lane.
+    const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
     auto stage = [&](int j, int slot) {  // 10 copies per wave
         const unsigned char* ph = reinterpret_cast<const unsigned char*>(
-            sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) + 8 * wave * kFragB + 16 * lane;
-        const unsigned char* ps = reinterpret_cast<const unsigned char*>(psi_at(j)) + 2 * wave * kFragB + 16 * lane;
+            sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) + 8 * wave * kFragB;
+        const unsigned char* ps = reinterpret_cast<const unsigned char*>(psi_at(j)) + 2 * wave * kFragB;
         lds_u8* dst = ring + slot * 4 * kScanSlot;
 #pragma unroll
-        for (int f = 0; f < 8; ++f) dma16(ph + f * kFragB, dst + f * kFragB);  // (rr, ks) = (f / 4, f % 4)
-        dma16(ps, dst + 8 * kFragB);
-        dma16(ps + kFragB, dst + 9 * kFragB);
+        for (int f = 0; f < 8; ++f) dma16(ph + f * kFragB, lane16, dst + f * kFragB);  // (rr, ks) = (f / 4, f % 4)
+        dma16(ps, lane16, dst + 8 * kFragB);
+        dma16(ps + kFragB, lane16, dst + 9 * kFragB);
     };
     // Every step issues one stage (clamped to the last step), so the copy for
     // step j always has exactly 2 (stores) + 10 + 2 operations after it when
@@ -908,10 +974,9 @@ __global__ void gdn_fill_zero_kernel(float* __restrict__ p, size_t n) {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-constexpr size_t kBytesT = 8 * 64 * 16;
-constexpr size_t kBytesA = 8 * 64 * 16;
-constexpr size_t kBytesK = 16 * 64 * 16;
-constexpr size_t kBytesG = 128 * 4;
+constexpr size_t kBytesT = 8 * 64 * 16;  // Tp fragments
+constexpr size_t kBytesA = 6 * 64 * 16;  // nonzero Aq fragments
+constexpr size_t kBytesG = 256 * 4;      // gate block
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -920,7 +985,7 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 // cannot fill the chip (each group then runs its own chain of chunks, joined
 // through the groups' affine maps).
 struct StatePlan {
-    int NT, NW_out, nvg_out, NW_map, nvg_map, G;
+    int NT, NW_out, nvg_out, NT_map, NW_map, nvg_map, G;
 };
 
 // `exact`: max_chunks is the exact chunk count of every sequence, so the
@@ -932,10 +997,20 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
     const int tiles = dv / (16 * s.NT);
     s.NW_out = (tiles % 4 == 0) ? 4 : (tiles % 2 == 0) ? 2 : 1;
     s.nvg_out = tiles / s.NW_out;
-    const int mtiles = (dv + kDK) / (16 * s.NT);
-    // At most 4 waves: with 8 a wave is held to 256 registers and spills.
-    s.NW_map = (mtiles % 4 == 0) ? 4 : (mtiles % 2 == 0) ? 2 : 1;
-    s.nvg_map = mtiles / s.NW_map;
+    // Map pass: one workgroup of 64-column waves for all dv + 128 columns
+    // when that is at most 4 waves (dv = 64, 128), so the shared operands are
+    // staged once per group; otherwise the output pass's tiling, at most 4
+    // waves per workgroup (with 8 a wave is held to 256 registers and spills).
+    if ((dv + kDK) % 64 == 0 && (dv + kDK) / 64 <= 4) {
+        s.NT_map = 4;
+        s.NW_map = (dv + kDK) / 64;
+        s.nvg_map = 1;
+    } else {
+        s.NT_map = s.NT;
+        const int mtiles = (dv + kDK) / (16 * s.NT);
+        s.NW_map = (mtiles % 4 == 0) ? 4 : (mtiles % 2 == 0) ? 2 : 1;
+        s.nvg_map = mtiles / s.NW_map;
+    }
     const long long base = nheads * s.nvg_out;  // output-pass workgroups with one group
     long long G = 1;
     if (base < 256 && max_chunks >= 8) G = std::min<long long>(std::min<long long>(16, 256 / base), max_chunks / 4);
@@ -945,7 +1020,7 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
 }
 
 struct WsLayout {
-    size_t offT, offA, offK, offG, offPsi, offPhi, total;
+    size_t offT, offA, offG, offPsi, offPhi, total;
 };
 
 WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const StatePlan& sp) {
@@ -953,8 +1028,7 @@ WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const State
     WsLayout L;
     L.offT = 0;
     L.offA = align256(L.offT + ch * kBytesT);
-    L.offK = align256(L.offA + ch * kBytesA);
-    L.offG = align256(L.offK + ch * kBytesK);
+    L.offG = align256(L.offA + ch * kBytesA);
     L.offPsi = align256(L.offG + ch * kBytesG);
     const size_t units = sp.G > 1 ? static_cast<size_t>(nheads) * sp.G : 0;
     L.offPhi = align256(L.offPsi + units * kDK * dv * 4);
@@ -980,6 +1054,12 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
         case 1: hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 1, NT>), grid, dim3(64), 0, stream, p, sg); break;
         case 2: hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 2, NT>), grid, dim3(128), 0, stream, p, sg); break;
         case 4: hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 4, NT>), grid, dim3(256), 0, stream, p, sg); break;
+        case 3:
+            if constexpr (MODE == kModeMap && NT == 4) {
+                hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 3, NT>), grid, dim3(192), 0, stream, p, sg);
+                break;
+            }
+            return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
         default:
             return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
     }
@@ -1001,7 +1081,6 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     char* ws = static_cast<char*>(workspace);
     p.wsT = reinterpret_cast<u32x4*>(ws + L.offT);
     p.wsA = reinterpret_cast<u32x4*>(ws + L.offA);
-    p.wsK = reinterpret_cast<u32x4*>(ws + L.offK);
     p.wsG = reinterpret_cast<float*>(ws + L.offG);
 
     if ((phases & 1) && nchunk_grid > 0) {
@@ -1020,8 +1099,9 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
         sg.nvg = sp.nvg_map;
         sg.ngroups_run = sp.G - 1;
         sg.xcd_map = ((nheads * sg.ngroups_run) % 8 == 0) ? 1 : 0;
-        st = sp.NT == 2 ? launch_state<kModeMap, 2>(p, sg, sp.NW_map, stream)
-                        : launch_state<kModeMap, 1>(p, sg, sp.NW_map, stream);
+        st = sp.NT_map == 4   ? launch_state<kModeMap, 4>(p, sg, sp.NW_map, stream)
+             : sp.NT_map == 2 ? launch_state<kModeMap, 2>(p, sg, sp.NW_map, stream)
+                              : launch_state<kModeMap, 1>(p, sg, sp.NW_map, stream);
         if (st != GDN_OK) return st;
         const long long nscan = nheads * (p.dv / 16);
         if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
@@ -1074,8 +1154,9 @@ int prefill_batch(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
     if (B == 0) return GDN_OK;
     if (!q || !k || !v || !A_log || !a || !b_logits || !state_out || (T > 0 && !out))
         return fail(GDN_ERR_INVALID_ARGUMENT, "prefill: null pointer argument");
-    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(state_out, 4) || (state_in && !aligned(state_in, 4)))
-        return fail(GDN_ERR_INVALID_ARGUMENT, "prefill: q/k need 16-byte alignment");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || (out && !aligned(out, 16)) ||
+        !aligned(state_out, 4) || (state_in && !aligned(state_in, 4)))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "prefill: q/k/v/out need 16-byte alignment");
     if (static_cast<long long>(B) * H * T * dv >= (1LL << 40))
         return fail(GDN_ERR_UNSUPPORTED, "prefill: problem too large");
     PrefillParams p = {};
@@ -1156,8 +1237,8 @@ int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_b
     if (num_seqs == 0) return GDN_OK;
     if (!q || !k || !v || !A_log || !a || !b_logits || !cu_seqlens || !state_out || (T_total > 0 && !out))
         return fail(GDN_ERR_INVALID_ARGUMENT, "prefill_varlen: null pointer argument");
-    if (!aligned(q, 16) || !aligned(k, 16))
-        return fail(GDN_ERR_INVALID_ARGUMENT, "prefill_varlen: q/k need 16-byte alignment");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || (out && !aligned(out, 16)))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "prefill_varlen: q/k/v/out need 16-byte alignment");
     if (static_cast<long long>(H) * T_total * dv >= (1LL << 40))
         return fail(GDN_ERR_UNSUPPORTED, "prefill_varlen: problem too large");
     PrefillParams p = {};
