@@ -576,33 +576,32 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
         }
     }
     bf16x8 tf[8], af[St::out ? 6 : 1], ktf[8][2];
-    // Tp and Kt for (c) and (e), read while (a) drains.
+    // With one wave per SIMD (NW <= 4) the Kt fragments are read here, while
+    // (a) drains; with two (NW = 8) the other wave covers their latency, so
+    // they are read just before (e) to keep this wave within 256 registers.
+    constexpr bool kEarlyKt = NW <= 4;
+    auto load_kt = [&]() {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            ktf[r][0] = ktfrag(buf + St::offK, kt_lane, r, 0);
+            ktf[r][1] = ktfrag(buf + St::offK, kt_lane, r, 1);
+        }
+    };
 #pragma unroll
     for (int f = 0; f < 8; ++f) tf[f] = frag(buf, St::offT + f * kFragB, lane);
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        ktf[r][0] = ktfrag(buf + St::offK, kt_lane, r, 0);
-        ktf[r][1] = ktfrag(buf + St::offK, kt_lane, r, 1);
-    }
+    if constexpr (kEarlyKt) load_kt();
     // V in the accumulator layout (column n, rows 16 mt + 4 g + i): one
     // transposing read per (mt, nt) -- source lane 4 j + a of group g reads
-    // row 16 mt + 4 g + j at columns 16 nt + 4 a .. + 3.
-    float vv[NT][16];
+    // row 16 mt + 4 g + j at columns 16 nt + 4 a .. + 3.  Kept as bf16 until use.
+    i16x4 vv[NT][4];
     const lds_u8* vrow = reinterpret_cast<const lds_u8*>(Vs) + ((4 * g + ((lane >> 2) & 3)) * 16 * NT + 4 * (lane & 3)) * 2;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            if (v_zero) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) vv[nt][4 * mt + i] = 0.f;
-            } else {
-                const i16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(vrow + (16 * mt * 16 * NT + 16 * nt) * 2));
-#pragma unroll
-                for (int i = 0; i < 4; ++i) vv[nt][4 * mt + i] = bf2f(static_cast<uint16_t>(t[i]));
-            }
-        }
+        for (int mt = 0; mt < 4; ++mt)
+            vv[nt][mt] = v_zero ? i16x4{0, 0, 0, 0}
+                                : __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                      (lds_i16x4*)(vrow + (16 * mt * 16 * NT + 16 * nt) * 2));
     f32x4 gam[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
@@ -613,7 +612,8 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) X[mt][nt][i] = vv[nt][4 * mt + i] - gam[mt][i] * X[mt][nt][i];
+            for (int i = 0; i < 4; ++i)
+                X[mt][nt][i] = bf2f(static_cast<uint16_t>(vv[nt][mt][i])) - gam[mt][i] * X[mt][nt][i];
     // (c) dV = Tp Y.
     f32x4 D[4][NT];
 #pragma unroll
@@ -645,6 +645,7 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
         BS0[nt] = pack8(kd[0] * D[0][nt], kd[1] * D[1][nt]);
         BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
     }
+    if constexpr (!kEarlyKt) load_kt();
     // (e) S <- gamma_C S + K^T (decay o dV)  (issued before (d): the recurrence's critical path).
 #pragma unroll
     for (int r = 0; r < 8; ++r)
@@ -985,7 +986,7 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 // cannot fill the chip (each group then runs its own chain of chunks, joined
 // through the groups' affine maps).
 struct StatePlan {
-    int NT, NW_out, nvg_out, NT_map, NW_map, nvg_map, G;
+    int NT_out, NW_out, nvg_out, NT_map, NW_map, nvg_map, G;
 };
 
 // `exact`: max_chunks is the exact chunk count of every sequence, so the
@@ -993,21 +994,31 @@ struct StatePlan {
 // untrimmed count, which never decreases as sequences grow.
 StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact) {
     StatePlan s;
-    s.NT = (dv % 32 == 0) ? 2 : 1;
-    const int tiles = dv / (16 * s.NT);
-    s.NW_out = (tiles % 4 == 0) ? 4 : (tiles % 2 == 0) ? 2 : 1;
-    s.nvg_out = tiles / s.NW_out;
-    // Map pass: one workgroup of 64-column waves for all dv + 128 columns
-    // when that is at most 4 waves (dv = 64, 128), so the shared operands are
-    // staged once per group; otherwise the output pass's tiling, at most 4
-    // waves per workgroup (with 8 a wave is held to 256 registers and spills).
-    if ((dv + kDK) % 64 == 0 && (dv + kDK) / 64 <= 4) {
+    // Two waves per SIMD (8-wave workgroups) where the tiling allows: the
+    // waves hide each other's LDS and copy latency.  The output pass then
+    // uses 16-column waves, the map pass 32-column waves, both within 256
+    // registers a wave.  Otherwise one wave per SIMD with wider tiles.
+    if (dv % 128 == 0) {
+        s.NT_out = 1;
+        s.NW_out = 8;
+    } else {
+        s.NT_out = (dv % 32 == 0) ? 2 : 1;
+        const int tiles = dv / (16 * s.NT_out);
+        s.NW_out = (tiles % 4 == 0) ? 4 : (tiles % 2 == 0) ? 2 : 1;
+    }
+    s.nvg_out = dv / (16 * s.NT_out * s.NW_out);
+    if ((dv + kDK) % 256 == 0) {
+        s.NT_map = 2;
+        s.NW_map = 8;
+        s.nvg_map = (dv + kDK) / 256;
+    } else if ((dv + kDK) % 64 == 0 && (dv + kDK) / 64 <= 4) {
+        // One workgroup of 64-column waves for all dv + 128 columns (dv = 64).
         s.NT_map = 4;
         s.NW_map = (dv + kDK) / 64;
         s.nvg_map = 1;
     } else {
-        s.NT_map = s.NT;
-        const int mtiles = (dv + kDK) / (16 * s.NT);
+        s.NT_map = (dv % 32 == 0) ? 2 : 1;
+        const int mtiles = (dv + kDK) / (16 * s.NT_map);
         s.NW_map = (mtiles % 4 == 0) ? 4 : (mtiles % 2 == 0) ? 2 : 1;
         s.nvg_map = mtiles / s.NW_map;
     }
@@ -1057,6 +1068,12 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
         case 3:
             if constexpr (MODE == kModeMap && NT == 4) {
                 hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 3, NT>), grid, dim3(192), 0, stream, p, sg);
+                break;
+            }
+            return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
+        case 8:
+            if constexpr ((MODE == kModeMap && NT == 2) || (MODE == kModeOut && NT == 1)) {
+                hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 8, NT>), grid, dim3(512), 0, stream, p, sg);
                 break;
             }
             return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
@@ -1112,8 +1129,8 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     sg.nvg = sp.nvg_out;
     sg.ngroups_run = sp.G;
     sg.xcd_map = ((nheads * sp.G) % 8 == 0) ? 1 : 0;
-    return sp.NT == 2 ? launch_state<kModeOut, 2>(p, sg, sp.NW_out, stream)
-                      : launch_state<kModeOut, 1>(p, sg, sp.NW_out, stream);
+    return sp.NT_out == 2 ? launch_state<kModeOut, 2>(p, sg, sp.NW_out, stream)
+                          : launch_state<kModeOut, 1>(p, sg, sp.NW_out, stream);
 }
 
 }  // namespace
