@@ -125,9 +125,9 @@ constexpr int kKLD = kDK + 8;  // padded LDS row (bf16) for K and Q tiles
 constexpr int kAQ = kC / 4 + 4;  // A stored by column, de-interleaved: Ad[j][i % 4][i / 4], padded
 constexpr int kBLD = kC + 8;   // padded LDS row (bf16) for 64x64 tiles
 
-// LDS use (about 73 KiB) allows two workgroups per CU, i.e. two waves per
-// SIMD: saying so lets the scheduler spend registers on hoisting LDS loads.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gdn_prefill_intra_kernel(
+// LDS use (about 47 KiB) allows three workgroups per CU, i.e. three waves
+// per SIMD: saying so lets the scheduler spend registers on hoisting loads.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gdn_prefill_intra_kernel(
     PrefillParams p) {
     const int c = blockIdx.x;
     const int h = blockIdx.y;
@@ -144,12 +144,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const size_t row_base = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0 + t0;
     const size_t wc = static_cast<size_t>(sq.slot0 + c) * p.H + h;
 
+    // The K tile is dead after step 3; T (step 5) reuses its space.
     __shared__ __attribute__((aligned(16))) bf16 Kl[kC][kKLD];
-    __shared__ __attribute__((aligned(16))) bf16 Ql[kC][kKLD];
     __shared__ __attribute__((aligned(16))) float Ad[kC][4][kAQ];
     __shared__ __attribute__((aligned(16))) bf16 Al[kC][kBLD];
-    __shared__ __attribute__((aligned(16))) bf16 Tl[kC][kBLD];
-    __shared__ float s_lgc[kC], s_bm[kC], s_ms[kC];
+    __shared__ float s_lg2[kC], s_bm[kC], s_ms[kC];  // s_lg2: in-chunk log2 decay cumsum
+    bf16(*const Tl)[kBLD] = reinterpret_cast<bf16(*)[kBLD]>(&Kl[0][0]);
+    static_assert(sizeof(Kl) >= sizeof(bf16) * kC * kBLD, "T tile must fit in the K tile");
 
     // Gate inputs (wave 0, one token per lane) are read first so their
     // latency overlaps the K/Q tile loads.
@@ -162,19 +163,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         g_b = bf2f(p.b[gi]);
     }
 
-    // 1) K and Q tiles into LDS; rows past the sequence end are zero.
+    // 1) K tile into LDS (rows past the sequence end are zero); Q goes
+    //    straight into MFMA A-operand registers, qf[ti][s] = Q[16 ti + m][32 s
+    //    + 8 g ..], rows clamped to the sequence (those rows get a zero output
+    //    coefficient below).
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int idx = tid + 256 * it;
         const int row = idx >> 4;
         const int c8 = (idx & 15) * 8;
-        u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u};
-        if (row < nvalid) {
-            kv = *reinterpret_cast<const u32x4*>(p.k + (row_base + row) * kDK + c8);
-            qv = *reinterpret_cast<const u32x4*>(p.q + (row_base + row) * kDK + c8);
-        }
+        u32x4 kv = {0u, 0u, 0u, 0u};
+        if (row < nvalid) kv = *reinterpret_cast<const u32x4*>(p.k + (row_base + row) * kDK + c8);
         *reinterpret_cast<u32x4*>(&Kl[row][c8]) = kv;
-        *reinterpret_cast<u32x4*>(&Ql[row][c8]) = qv;
+    }
+    bf16x8 qf[4][4];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+        const uint16_t* qr = p.q + (row_base + min(16 * ti + m16, nvalid - 1)) * kDK + 8 * g4;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qf[ti][s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
 
     // 2) Gates (wave 0, one token per lane) and the in-chunk log-cumsum.
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         }
         const float s = wave_inclusive_sum(lg);
         const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), kWave - 1));
-        s_lgc[t] = s;
+        s_lg2[t] = s * 1.4426950408889634f;  // log2(e)
         s_bm[t] = bm;
         s_ms[t] = m * p.scale;
         const float gam = expf(s);
@@ -217,16 +224,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const bf16x8 aK = *reinterpret_cast<const bf16x8*>(&Kl[16 * ti + m16][32 * s + 8 * g4]);
-            const bf16x8 aQ = *reinterpret_cast<const bf16x8*>(&Ql[16 * ti + m16][32 * s + 8 * g4]);
             const bf16x8 bK = *reinterpret_cast<const bf16x8*>(&Kl[16 * tj + m16][32 * s + 8 * g4]);
             accK = mfma16x16x32(aK, bK, accK);
-            accQ = mfma16x16x32(aQ, bK, accQ);
+            accQ = mfma16x16x32(qf[ti][s], bK, accQ);
         }
-        const float lgc_col = s_lgc[col];
+        const float lg2_col = s_lg2[col];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * ti + 4 * g4 + i;
-            const float d = expf(s_lgc[row] - lgc_col);
+            const float d = __builtin_amdgcn_exp2f(s_lg2[row] - lg2_col);  // Gamma_{row,col}
             Ad[col][row & 3][row >> 2] = row > col ? s_bm[row] * accK[i] * d : 0.f;
             Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
         }
