@@ -70,6 +70,8 @@ struct PrefillParams {
     int T_stride;        // tokens per (b, h) row block of q/k/v/a/b/out
     int T_len;           // batch mode: sequence length
     int chunks_per_seq;  // batch mode: ceil(T_len / 64)
+    int xcd_heads;       // (sequence, head) pairs are a multiple of 8: head-aligned XCD mapping
+    int nchunk_grid;     // intra kernel: chunks per (sequence, head) in the grid
 };
 
 struct SeqInfo {
@@ -96,6 +98,19 @@ __device__ __forceinline__ SeqInfo seq_info(const PrefillParams& p, int sidx) {
 
 __device__ __forceinline__ int pi_pos(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4); }
 __device__ __forceinline__ int rho_row(int r, int g, int i) { return 32 * (r >> 1) + 8 * g + 4 * (r & 1) + i; }
+
+// Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD
+// has its own L2.  With a multiple of 8 (sequence, head) pairs every prefill
+// kernel puts head `hd` on XCD hd % 8, so what one kernel writes for a head
+// is read from the same L2 by the next: linear id L -> head (L % 8) + 8 q,
+// item r of that head, where L / 8 = q * per_head + r.
+struct HeadItem {
+    int head, item;
+};
+__device__ __forceinline__ HeadItem head_major_xcd(int L, int per_head) {
+    const int q = (L >> 3) / per_head;
+    return {(L & 7) + 8 * q, (L >> 3) - q * per_head};
+}
 
 // The nonzero fragments (mt, s) of the causal Aq, in workspace order:
 // (0,0),(1,0),(2,0),(2,1),(3,0),(3,1) as f = 2 mt + s.
@@ -129,9 +144,17 @@ constexpr int kBLD = kC + 8;   // padded LDS row (bf16) for 64x64 tiles
 // per SIMD: saying so lets the scheduler spend registers on hoisting loads.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gdn_prefill_intra_kernel(
     PrefillParams p) {
-    const int c = blockIdx.x;
-    const int h = blockIdx.y;
-    const int sidx = blockIdx.z;
+    int c, h, sidx;
+    if (p.xcd_heads) {  // 1-D grid, head-aligned XCD mapping
+        const HeadItem hi = head_major_xcd(blockIdx.x, p.nchunk_grid);
+        c = hi.item;
+        sidx = hi.head / p.H;
+        h = hi.head % p.H;
+    } else {
+        c = blockIdx.x;
+        h = blockIdx.y;
+        sidx = blockIdx.z;
+    }
     const SeqInfo sq = seq_info(p, sidx);
     const int t0 = c * kC;
     if (t0 >= sq.len) return;  // uniform over the workgroup
@@ -176,12 +199,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         if (row < nvalid) kv = *reinterpret_cast<const u32x4*>(p.k + (row_base + row) * kDK + c8);
         *reinterpret_cast<u32x4*>(&Kl[row][c8]) = kv;
     }
-    bf16x8 qf[4][4];
+    // Step 3's tiles are dealt so that wave w needs Q row block w and, for
+    // w < 2, row block 3: qa = block w, qb = block 3.
+    bf16x8 qa[4], qb[4];
+    {
+        const uint16_t* qr = p.q + (row_base + min(16 * wave + m16, nvalid - 1)) * kDK + 8 * g4;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-        const uint16_t* qr = p.q + (row_base + min(16 * ti + m16, nvalid - 1)) * kDK + 8 * g4;
+        for (int s = 0; s < 4; ++s) qa[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
+    }
+    if (wave < 2) {
+        const uint16_t* qr = p.q + (row_base + min(48 + m16, nvalid - 1)) * kDK + 8 * g4;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) qf[ti][s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
+        for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
 
     // 2) Gates (wave 0, one token per lane) and the in-chunk log-cumsum.
@@ -206,27 +235,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     __syncthreads();
 
-    // 3) K K^T and Q K^T on the 10 lower 16x16 tiles (i >= j), dealt round
-    //    robin to the 4 waves; the 6 upper tiles of Aq are zeroed.
+    // 3) K K^T and Q K^T on the 10 lower 16x16 tiles (i >= j): tile (ti, tj)
+    //    goes to wave ti, except (3,0), (3,1) to wave 0 and (3,2) to wave 1
+    //    (three tiles each for waves 0-2); wave 3 takes (3,3) and zeroes the 6
+    //    upper tiles of Aq.
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
         const int ti = t >> 2, tj = t & 3;  // tile (row ti, col tj)
-        const int order = ti * (ti + 1) / 2 + tj;  // index among lower tiles
         const int col = 16 * tj + m16;
         if (tj > ti) {
-            if ((t - 10 + 16) % 4 != wave) continue;
+            if (wave != 3) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) Al[16 * ti + 4 * g4 + i][col] = f2bf(0.f);
             continue;
         }
-        if (order % 4 != wave) continue;
+        const int owner = ti < 3 ? ti : (tj < 2 ? 0 : (tj == 2 ? 1 : 3));
+        if (owner != wave) continue;
         f32x4 accK = {0.f, 0.f, 0.f, 0.f}, accQ = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const bf16x8 aK = *reinterpret_cast<const bf16x8*>(&Kl[16 * ti + m16][32 * s + 8 * g4]);
             const bf16x8 bK = *reinterpret_cast<const bf16x8*>(&Kl[16 * tj + m16][32 * s + 8 * g4]);
             accK = mfma16x16x32(aK, bK, accK);
-            accQ = mfma16x16x32(qf[ti][s], bK, accQ);
+            accQ = mfma16x16x32(ti == wave ? qa[s] : qb[s], bK, accQ);
         }
         const float lg2_col = s_lg2[col];
 #pragma unroll
@@ -345,6 +376,7 @@ struct Stage {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 typedef __attribute__((address_space(3))) float lds_f32;
@@ -711,7 +743,6 @@ struct StateGrid {
     int ngroups;     // chunk groups per sequence (G)
     int ngroups_run; // groups per sequence this launch covers (map pass: G - 1)
     int nheads;      // sequences x heads
-    int xcd_map;     // deal the workgroups of one (head, group) to one XCD
     float* psi;      // [nheads][G][dv/16][8][64][4] fp32 (16-column tile, accumulator tile r,
                      // lane, slot): map pass zero-state results, then (scan) the initial
                      // state of group j + 1 in slot j
@@ -739,17 +770,18 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 
     const int wg = blockIdx.x;
     const int nunits = sg.nheads * sg.ngroups_run;
-    int unit, vg;
-    if (sg.xcd_map) {
-        const int xcd = wg & 7, j = wg >> 3;
-        vg = j % sg.nvg;
-        unit = (j / sg.nvg) * 8 + xcd;
+    int head, grp, vg;
+    if (p.xcd_heads) {
+        const HeadItem hi = head_major_xcd(wg, sg.ngroups_run * sg.nvg);
+        head = hi.head;
+        grp = hi.item / sg.nvg;
+        vg = hi.item % sg.nvg;
     } else {
         vg = wg % sg.nvg;
-        unit = wg / sg.nvg;
+        head = (wg / sg.nvg) / sg.ngroups_run;
+        grp = (wg / sg.nvg) % sg.ngroups_run;
     }
-    if (unit >= nunits) return;  // uniform over the workgroup
-    const int head = unit / sg.ngroups_run, grp = unit % sg.ngroups_run;
+    if (head * sg.ngroups_run + grp >= nunits) return;  // uniform over the workgroup
     const int sidx = head / p.H;
     const int h = head % p.H;
     const SeqInfo sq = seq_info(p, sidx);
@@ -877,94 +909,113 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 }
 
 // Initial states of the chunk groups: S_in(0) = state_in (or 0) and
-// S_in(j + 1) = phi_j S_in(j) + psi_j, written over psi_j.  One workgroup per
-// (sequence-head, 16-column tile); wave w owns state rows 32w .. 32w + 31 (row
-// tiles 2w and 2w + 1 of the accumulator order), which are exactly the rows of
-// MFMA k-step w, so each wave publishes its rows as that k-step's B operand
-// (bf16 high and low halves of the fp32 state) and reads all four back.  Each
-// wave copies its own rows of phi_j and psi_j into an LDS ring kScanRing - 1
-// steps ahead (asynchronous copies, waited for with explicit counts).
+// S_in(j + 1) = phi_j S_in(j) + psi_j, written over psi_j.  One workgroup of
+// 8 waves per (sequence-head, 16-column tile); wave w owns accumulator row
+// tile r = w (state rows rho(w, g, i)).  Row tiles 2s and 2s + 1 make up
+// MFMA k-step s, so wave w publishes its rows as one 8-byte half of k-step
+// w / 2's B operand (bf16 high and low parts of the fp32 state, which give
+// two independent accumulation chains) and every wave reads all four k-steps
+// back.  Each wave copies its own phi fragments and psi quad into an LDS ring
+// kScanRing - 1 steps ahead (asynchronous copies, explicit wait counts).
 constexpr int kScanRing = 3;
-constexpr int kScanSlot = 10 * kFragB;  // per wave and step: 8 phi fragments, 2 psi quads
+constexpr int kScanSlot = 5 * kFragB;  // per wave and step: 4 phi fragments, 1 psi quad
 
-__global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(PrefillParams p, StateGrid sg) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * 8 * kFragB + kScanRing * 4 * kScanSlot];
+__device__ __forceinline__ u32x2 pack4_hi(const f32x4 v) {
+    u32x2 r;
+    r[0] = static_cast<uint32_t>(f2bf_bits(v[0])) | (static_cast<uint32_t>(f2bf_bits(v[1])) << 16);
+    r[1] = static_cast<uint32_t>(f2bf_bits(v[2])) | (static_cast<uint32_t>(f2bf_bits(v[3])) << 16);
+    return r;
+}
+// bf16 of (x - bf16(x)): the low part of a two-term bf16 split.
+__device__ __forceinline__ u32x2 pack4_lo(const f32x4 v, const u32x2 hi) {
+    f32x4 d;
+    d[0] = v[0] - __uint_as_float(hi[0] << 16);
+    d[1] = v[1] - __uint_as_float(hi[0] & 0xffff0000u);
+    d[2] = v[2] - __uint_as_float(hi[1] << 16);
+    d[3] = v[3] - __uint_as_float(hi[1] & 0xffff0000u);
+    return pack4_hi(d);
+}
+
+__global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, StateGrid sg) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * 8 * kFragB + kScanRing * 8 * kScanSlot];
     const int dv = p.dv, ntile = dv / 16;
     const int nunits = sg.nheads * ntile;
     const int steps = sg.ngroups - 1;
-    int u = blockIdx.x;
-    if (u >= nunits || steps <= 0) return;  // uniform over the workgroup
-    if (nunits % 8 == 0) u = (u & 7) * (nunits >> 3) + (u >> 3);  // one head's tiles on one XCD
-    const int head = u / ntile, tile = u % ntile;
+    if (static_cast<int>(blockIdx.x) >= nunits || steps <= 0) return;  // uniform over the workgroup
+    int head, tile;
+    if (p.xcd_heads) {
+        const HeadItem hi = head_major_xcd(blockIdx.x, ntile);
+        head = hi.head;
+        tile = hi.item;
+    } else {
+        head = blockIdx.x / ntile;
+        tile = blockIdx.x % ntile;
+    }
     const int sidx = head / p.H, h = head % p.H;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = row tile r
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
     const int col = 16 * tile + n;
     lds_u8* const sbuf = (lds_u8*)&smem[0];
     lds_u8* const ring = (lds_u8*)&smem[2 * 8 * kFragB] + wave * kScanSlot;
 
-    f32x4 S[2];
+    f32x4 S;
     if (p.state_in) {
         const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) S[rr][i] = sin[rho_row(2 * wave + rr, g, i) * dv + col];
+        for (int i = 0; i < 4; ++i) S[i] = sin[rho_row(wave, g, i) * dv + col];
     } else {
-        S[0] = S[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        S = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     auto psi_at = [&](int j) {
         return sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048;
     };
-    // This wave's phi fragments (row tiles 2w, 2w + 1: 8 contiguous KiB) and
-    // psi quads (2 contiguous KiB); every copy reads 1 KiB, 16 bytes a lane.
+    // This wave's phi fragments (row tile r, k-steps 0..3: 4 contiguous KiB)
+    // and psi quad r (1 KiB); every copy reads 1 KiB, 16 bytes a lane.
     const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
-    auto stage = [&](int j, int slot) {  // 10 copies per wave
+    auto stage = [&](int j, int slot) {  // 5 copies per wave
         const unsigned char* ph = reinterpret_cast<const unsigned char*>(
-            sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) + 8 * wave * kFragB;
-        const unsigned char* ps = reinterpret_cast<const unsigned char*>(psi_at(j)) + 2 * wave * kFragB;
-        lds_u8* dst = ring + slot * 4 * kScanSlot;
+            sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) + 4 * wave * kFragB;
+        lds_u8* dst = ring + slot * 8 * kScanSlot;
 #pragma unroll
-        for (int f = 0; f < 8; ++f) dma16(ph + f * kFragB, lane16, dst + f * kFragB);  // (rr, ks) = (f / 4, f % 4)
-        dma16(ps, lane16, dst + 8 * kFragB);
-        dma16(ps + kFragB, lane16, dst + 9 * kFragB);
+        for (int ks = 0; ks < 4; ++ks) dma16(ph + ks * kFragB, lane16, dst + ks * kFragB);
+        dma16(reinterpret_cast<const unsigned char*>(psi_at(j)) + wave * kFragB, lane16, dst + 4 * kFragB);
     };
     // Every step issues one stage (clamped to the last step), so the copy for
-    // step j always has exactly 2 (stores) + 10 + 2 operations after it when
-    // step j begins, for kScanRing = 3.
+    // step j always has exactly 1 (store) + 5 + 1 operations after it when
+    // step j begins, for kScanRing = 3.  A step's stage is issued right after
+    // its MFMAs, so copy issue overlaps their latency instead of preceding them.
     static_assert(kScanRing == 3, "wait count below assumes a 3-deep ring");
 #pragma unroll
     for (int d = 0; d < kScanRing - 1; ++d) stage(min(d, steps - 1), d);
+    const int half = (wave & 1) * 8;  // this row tile's bytes in its k-step's B fragment
+    auto publish = [&](lds_u8* buf) {
+        const u32x2 hi = pack4_hi(S);
+        *reinterpret_cast<lds_u32x2*>(buf + (2 * (wave >> 1)) * kFragB + 16 * lane + half) = hi;
+        *reinterpret_cast<lds_u32x2*>(buf + (2 * (wave >> 1) + 1) * kFragB + 16 * lane + half) = pack4_lo(S, hi);
+    };
+    publish(sbuf);
     for (int j = 0; j < steps; ++j) {
         const int slot = j % kScanRing;
         lds_u8* const buf = sbuf + (j & 1) * 8 * kFragB;
-        const bf16x8 hi = pack8(S[0], S[1]);
-        *reinterpret_cast<lds_bf16x8*>(buf + (2 * wave) * kFragB + 16 * lane) = hi;
-        *reinterpret_cast<lds_bf16x8*>(buf + (2 * wave + 1) * kFragB + 16 * lane) = pack8_lo(S[0], S[1], hi);
         if (j == 0)
-            wait_vm<10>();  // the first stage; the second may still be in flight
+            wait_vm<5>();  // the first stage; the second may still be in flight
         else
-            wait_vm<14>();
+            wait_vm<7>();
         lds_barrier();
-        stage(min(j + kScanRing - 1, steps - 1), (j + kScanRing - 1) % kScanRing);
-        const lds_u8* src = ring + slot * 4 * kScanSlot;
-        f32x4 acc[2] = {*reinterpret_cast<const lds_f32x4*>(src + 8 * kFragB + 16 * lane),
-                        *reinterpret_cast<const lds_f32x4*>(src + 9 * kFragB + 16 * lane)};
+        const lds_u8* src = ring + slot * 8 * kScanSlot;
+        f32x4 acc_h = *reinterpret_cast<const lds_f32x4*>(src + 4 * kFragB + 16 * lane);
+        f32x4 acc_l = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const bf16x8 bh = frag(buf, (2 * ks) * kFragB, lane);
-            const bf16x8 bl = frag(buf, (2 * ks + 1) * kFragB, lane);
-#pragma unroll
-            for (int rr = 0; rr < 2; ++rr) {
-                const bf16x8 a = frag(src, (4 * rr + ks) * kFragB, lane);
-                acc[rr] = mfma16x16x32(a, bh, acc[rr]);
-                acc[rr] = mfma16x16x32(a, bl, acc[rr]);
-            }
+            const bf16x8 a = frag(src, ks * kFragB, lane);
+            acc_h = mfma16x16x32(a, frag(buf, (2 * ks) * kFragB, lane), acc_h);
+            acc_l = mfma16x16x32(a, frag(buf, (2 * ks + 1) * kFragB, lane), acc_l);
         }
-        f32x4* out = reinterpret_cast<f32x4*>(psi_at(j)) + 2 * wave * 64 + lane;
-        out[0] = S[0] = acc[0];
-        out[64] = S[1] = acc[1];
+        stage(min(j + kScanRing - 1, steps - 1), (j + kScanRing - 1) % kScanRing);
+        S = acc_h + acc_l;
+        reinterpret_cast<f32x4*>(psi_at(j))[wave * 64 + lane] = S;
+        publish(sbuf + ((j + 1) & 1) * 8 * kFragB);
     }
     wait_vm<0>();  // the clamped trailing copies land before the workgroup's LDS is released
 }
@@ -1064,7 +1115,7 @@ int check_common(const char* who, int H, int dk, int dv) {
 
 template <int MODE, int NT>
 int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_t stream) {
-    const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups * sg.nvg;
+    const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups_run * sg.nvg;
     if (nwg > 0x7fffffffLL) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
     const dim3 grid(static_cast<unsigned>(nwg));
     switch (NW) {
@@ -1106,8 +1157,16 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     p.wsA = reinterpret_cast<u32x4*>(ws + L.offA);
     p.wsG = reinterpret_cast<float*>(ws + L.offG);
 
+    p.xcd_heads = (nheads % 8 == 0) ? 1 : 0;
+    p.nchunk_grid = nchunk_grid;
     if ((phases & 1) && nchunk_grid > 0) {
-        hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(nchunk_grid, p.H, nseq), dim3(256), 0, stream, p);
+        if (p.xcd_heads) {
+            const long long nwg = nheads * nchunk_grid;
+            if (nwg > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
+            hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(nchunk_grid, p.H, nseq), dim3(256), 0, stream, p);
+        }
         const int st = gdn_host::check_launch("gdn_prefill_intra_kernel");
         if (st != GDN_OK) return st;
     }
@@ -1121,20 +1180,18 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     if (sp.G > 1) {
         sg.nvg = sp.nvg_map;
         sg.ngroups_run = sp.G - 1;
-        sg.xcd_map = ((nheads * sg.ngroups_run) % 8 == 0) ? 1 : 0;
         st = sp.NT_map == 4   ? launch_state<kModeMap, 4>(p, sg, sp.NW_map, stream)
              : sp.NT_map == 2 ? launch_state<kModeMap, 2>(p, sg, sp.NW_map, stream)
                               : launch_state<kModeMap, 1>(p, sg, sp.NW_map, stream);
         if (st != GDN_OK) return st;
         const long long nscan = nheads * (p.dv / 16);
         if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-        hipLaunchKernelGGL(gdn_prefill_scan_kernel, dim3(static_cast<unsigned>(nscan)), dim3(256), 0, stream, p, sg);
+        hipLaunchKernelGGL(gdn_prefill_scan_kernel, dim3(static_cast<unsigned>(nscan)), dim3(512), 0, stream, p, sg);
         st = gdn_host::check_launch("gdn_prefill_scan_kernel");
         if (st != GDN_OK) return st;
     }
     sg.nvg = sp.nvg_out;
     sg.ngroups_run = sp.G;
-    sg.xcd_map = ((nheads * sp.G) % 8 == 0) ? 1 : 0;
     return sp.NT_out == 2 ? launch_state<kModeOut, 2>(p, sg, sp.NW_out, stream)
                           : launch_state<kModeOut, 1>(p, sg, sp.NW_out, stream);
 }
