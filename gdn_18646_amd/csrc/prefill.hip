@@ -72,6 +72,7 @@ struct PrefillParams {
     int chunks_per_seq;  // batch mode: ceil(T_len / 64)
     int xcd_heads;       // (sequence, head) pairs are a multiple of 8: head-aligned XCD mapping
     int nchunk_grid;     // intra kernel: chunks per (sequence, head) in the grid
+    int intra_units;     // intra kernel: (sequence, head) pairs x nchunk_grid
 };
 
 struct SeqInfo {
@@ -140,32 +141,76 @@ constexpr int kKLD = kDK + 8;  // padded LDS row (bf16) for K and Q tiles
 constexpr int kAQ = kC / 4 + 4;  // A stored by column, de-interleaved: Ad[j][i % 4][i / 4], padded
 constexpr int kBLD = kC + 8;   // padded LDS row (bf16) for 64x64 tiles
 
+// One (chunk, sequence-head) unit of kernel 1.  Unit u maps to head, chunk
+// through head_major_xcd when the head count allows (the persistent grid is a
+// multiple of 8, so a workgroup's units all share its XCD).
+struct IntraUnit {
+    SeqInfo sq;
+    size_t row_base, wc;
+    int c, h, t0, nvalid;
+    bool valid;
+};
+__device__ __forceinline__ IntraUnit intra_unit(const PrefillParams& p, int u) {
+    IntraUnit U = {};
+    U.valid = false;
+    if (u >= p.intra_units) return U;
+    int head;
+    if (p.xcd_heads) {
+        const HeadItem hi = head_major_xcd(u, p.nchunk_grid);
+        head = hi.head;
+        U.c = hi.item;
+    } else {
+        head = u / p.nchunk_grid;
+        U.c = u % p.nchunk_grid;
+    }
+    U.h = head % p.H;
+    U.sq = seq_info(p, head / p.H);
+    U.t0 = U.c * kC;
+    if (U.t0 >= U.sq.len) return U;  // varlen: past this sequence's end
+    U.valid = true;
+    U.nvalid = min(kC, U.sq.len - U.t0);
+    U.row_base = static_cast<size_t>(U.sq.b * p.H + U.h) * p.T_stride + U.sq.tok0 + U.t0;
+    U.wc = static_cast<size_t>(U.sq.slot0 + U.c) * p.H + U.h;
+    return U;
+}
+
+// A unit's global inputs that are prefetched into registers: the K tile slice
+// this thread stores to LDS (rows past the sequence end zero) and wave 0's
+// gate inputs (one token per lane).
+struct IntraLoads {
+    u32x4 kv[4];
+    float g_m, g_a, g_b;
+};
+__device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUnit& U, int tid, IntraLoads& L) {
+    const int wave = tid >> 6, lane = tid & 63;
+    L.g_m = L.g_a = L.g_b = 0.f;
+    if (wave == 0 && lane < U.nvalid) {
+        const size_t gi = U.row_base + lane;
+        L.g_m = p.mask ? p.mask[static_cast<size_t>(U.sq.b) * p.T_stride + U.sq.tok0 + U.t0 + lane] : 1.f;
+        L.g_a = bf2f(p.a[gi]);
+        L.g_b = bf2f(p.b[gi]);
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int idx = tid + 256 * it, row = idx >> 4, c8 = (idx & 15) * 8;
+        L.kv[it] = u32x4{0u, 0u, 0u, 0u};
+        if (row < U.nvalid) L.kv[it] = *reinterpret_cast<const u32x4*>(p.k + (U.row_base + row) * kDK + c8);
+    }
+}
+
+// Persistent: each workgroup walks units blockIdx.x, + gridDim.x, ...; the
+// next unit's K slice and gate inputs are loaded into registers (IntraLoads)
+// while the current unit's triangular solve runs, so global latency overlaps
+// compute.  Q (MFMA A operands of Q K^T) is read at the start of its unit.
 // LDS use (about 47 KiB) allows three workgroups per CU, i.e. three waves
 // per SIMD: saying so lets the scheduler spend registers on hoisting loads.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gdn_prefill_intra_kernel(
     PrefillParams p) {
-    int c, h, sidx;
-    if (p.xcd_heads) {  // 1-D grid, head-aligned XCD mapping
-        const HeadItem hi = head_major_xcd(blockIdx.x, p.nchunk_grid);
-        c = hi.item;
-        sidx = hi.head / p.H;
-        h = hi.head % p.H;
-    } else {
-        c = blockIdx.x;
-        h = blockIdx.y;
-        sidx = blockIdx.z;
-    }
-    const SeqInfo sq = seq_info(p, sidx);
-    const int t0 = c * kC;
-    if (t0 >= sq.len) return;  // uniform over the workgroup
-    const int nvalid = min(kC, sq.len - t0);
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const int m16 = lane & 15;
     const int g4 = lane >> 4;
-    const size_t row_base = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0 + t0;
-    const size_t wc = static_cast<size_t>(sq.slot0 + c) * p.H + h;
 
     // The K tile is dead after step 3; T (step 5) reuses its space.
     __shared__ __attribute__((aligned(16))) bf16 Kl[kC][kKLD];
@@ -175,40 +220,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     bf16(*const Tl)[kBLD] = reinterpret_cast<bf16(*)[kBLD]>(&Kl[0][0]);
     static_assert(sizeof(Kl) >= sizeof(bf16) * kC * kBLD, "T tile must fit in the K tile");
 
-    // Gate inputs (wave 0, one token per lane) are read first so their
-    // latency overlaps the K/Q tile loads.
-    const bool tok_ok = wave == 0 && lane < nvalid;
-    float g_m = 0.f, g_a = 0.f, g_b = 0.f;
-    if (tok_ok) {
-        const size_t gi = row_base + lane;
-        g_m = p.mask ? p.mask[static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + t0 + lane] : 1.f;
-        g_a = bf2f(p.a[gi]);
-        g_b = bf2f(p.b[gi]);
+    int u = blockIdx.x;
+    IntraUnit U = intra_unit(p, u);
+    IntraLoads L;
+    if (U.valid) intra_load(p, U, tid, L);
+    while (u < p.intra_units) {
+    const int u_next = u + static_cast<int>(gridDim.x);
+    const IntraUnit N = intra_unit(p, u_next);
+    if (!U.valid) {
+        if (N.valid) intra_load(p, N, tid, L);
+        u = u_next;
+        U = N;
+        continue;
     }
+    const int c = U.c, h = U.h, nvalid = U.nvalid;
+    const size_t wc = U.wc;
+    const bool tok_ok = wave == 0 && lane < nvalid;
+    const float g_m = L.g_m, g_a = L.g_a, g_b = L.g_b;
+    (void)c;
 
-    // 1) K tile into LDS (rows past the sequence end are zero); Q goes
-    //    straight into MFMA A-operand registers, qf[ti][s] = Q[16 ti + m][32 s
-    //    + 8 g ..], rows clamped to the sequence (those rows get a zero output
-    //    coefficient below).
+    // 1) K tile into LDS.
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int idx = tid + 256 * it;
-        const int row = idx >> 4;
-        const int c8 = (idx & 15) * 8;
-        u32x4 kv = {0u, 0u, 0u, 0u};
-        if (row < nvalid) kv = *reinterpret_cast<const u32x4*>(p.k + (row_base + row) * kDK + c8);
-        *reinterpret_cast<u32x4*>(&Kl[row][c8]) = kv;
+        *reinterpret_cast<u32x4*>(&Kl[idx >> 4][(idx & 15) * 8]) = L.kv[it];
     }
-    // Step 3's tiles are dealt so that wave w needs Q row block w and, for
-    // w < 2, row block 3: qa = block w, qb = block 3.
+    // Q row blocks as MFMA A operands: step 3's tiles are dealt so wave w
+    // needs block w (qa) and, for w < 2, block 3 (qb).  Rows are clamped to
+    // the sequence; those rows get a zero output coefficient.
     bf16x8 qa[4], qb[4];
     {
-        const uint16_t* qr = p.q + (row_base + min(16 * wave + m16, nvalid - 1)) * kDK + 8 * g4;
+        const uint16_t* qr = p.q + (U.row_base + min(16 * wave + m16, nvalid - 1)) * kDK + 8 * g4;
 #pragma unroll
         for (int s = 0; s < 4; ++s) qa[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
     if (wave < 2) {
-        const uint16_t* qr = p.q + (row_base + min(48 + m16, nvalid - 1)) * kDK + 8 * g4;
+        const uint16_t* qr = p.q + (U.row_base + min(48 + m16, nvalid - 1)) * kDK + 8 * g4;
 #pragma unroll
         for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
@@ -269,6 +316,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         }
     }
     __syncthreads();
+    // The current unit's inputs are consumed: start the next unit's loads.
+    if (N.valid) intra_load(p, N, tid, L);
 
     // 4) The six nonzero Aq fragments (mt, s) = (0,0),(1,0),(2,0),(2,1),(3,0),(3,1):
     //    lane holds Aq[16mt + m][32s + pi(g, j)].
@@ -290,25 +339,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     //    the quad, and every lane folds it into its later rows (independent
     //    FMAs, off the row-to-row chain).
     {
-        const int c = 16 * wave + (lane >> 2);
-        const int sub = lane & 3;
+        int c = 16 * wave + (lane >> 2);
+        int sub = lane & 3;
+        // Opaque per unit: otherwise the compiler hoists the 64 per-row
+        // selects on c and sub out of the persistent loop and spills them.
+        asm volatile("" : "+v"(c), "+v"(sub));
         float Tc[16], acc[16];
 #pragma unroll
         for (int q = 0; q < 16; ++q) Tc[q] = acc[q] = 0.f;
-        // Row j of A (this lane's slots) is loaded two rows ahead into a
-        // ring; the empty asm keeps the scheduler from sinking the loads back
-        // to their use, so LDS latency overlaps the previous rows' chain.
-        f32x4 ring[3][4];
+        // Row j of A (this lane's slots) is loaded a row ahead into a ring;
+        // the empty asm keeps the scheduler from sinking the loads back to
+        // their use, so LDS latency overlaps the previous row's chain.
+        f32x4 ring[2][4];
         auto load_row = [&](int j, f32x4 (&dst)[4]) {
 #pragma clang loop unroll(full)
             for (int q4 = (j >> 2) >> 2; q4 < 4; ++q4) dst[q4] = *reinterpret_cast<const f32x4*>(&Ad[j][sub][4 * q4]);
         };
         load_row(0, ring[0]);
-        load_row(1, ring[1]);
         // Fully unrolled (the row index must be a constant: Tc stays in registers).
 #pragma clang loop unroll(full)
         for (int j = 0; j < kC; ++j) {
-            if (j + 2 < kC) load_row(j + 2, ring[(j + 2) % 3]);
+            if (j + 1 < kC) load_row(j + 1, ring[(j + 1) % 2]);
             asm volatile("" ::: "memory");
             const int qj = j >> 2, sj = j & 3;
             const float own = (j == c ? 1.f : 0.f) - acc[qj];  // row j, valid in lane sub == sj
@@ -319,7 +370,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             else tj = dpp_f<0xFF>(own);               // quad_perm [3,3,3,3]
             Tc[qj] = sub == sj ? tj : Tc[qj];
             // Fold row j into rows i > j: slots q >= qj (slot qj only for sub > sj).
-            const f32x4(&a)[4] = ring[j % 3];
+            const f32x4(&a)[4] = ring[j % 2];
 #pragma clang loop unroll(full)
             for (int q4 = qj >> 2; q4 < 4; ++q4) {
 #pragma clang loop unroll(full)
@@ -344,6 +395,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
         p.wsT[(wc * 8 + f) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+    __syncthreads();  // T (aliasing the K tile) is read before the next unit's K is stored
+    u = u_next;
+    U = N;
     }
 }
 
@@ -1160,13 +1215,18 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     p.xcd_heads = (nheads % 8 == 0) ? 1 : 0;
     p.nchunk_grid = nchunk_grid;
     if ((phases & 1) && nchunk_grid > 0) {
-        if (p.xcd_heads) {
-            const long long nwg = nheads * nchunk_grid;
-            if (nwg > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-            hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p);
-        } else {
-            hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(nchunk_grid, p.H, nseq), dim3(256), 0, stream, p);
-        }
+        const long long units = nheads * nchunk_grid;
+        if (units > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
+        p.intra_units = static_cast<int>(units);
+        // Persistent grid: three workgroups per CU (LDS-limited), a multiple
+        // of 8 so each workgroup's units stay on its XCD.
+        int dev = 0, ncu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+        long long nwg = std::min<long long>(units, 3LL * ncu);
+        if (nwg >= 8) nwg &= ~7LL;
+        hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p);
         const int st = gdn_host::check_launch("gdn_prefill_intra_kernel");
         if (st != GDN_OK) return st;
     }
