@@ -9,10 +9,11 @@ with the achieved MFMA / HBM roofline fractions.
   in HBM.  One step = one ``prefill.prefill`` call (both kernels).
 * ``decode``: B=256, H=32, dk=dv=128, one 512 MiB fp32 state updated in place,
   100 consecutive steps with fresh q/k/v/a/b per step (inputs pre-staged).
-* ``roofline``: the prefill state-pass kernel (the dominant one) against bf16
-  MFMA peak; ``decode.roofline``: the decode kernel against HBM peak.  Kernel
-  durations come from HIP events around per-phase launches on the stream the
-  kernels run on.
+* ``roofline``: the prefill state phase (the GEMM phase: map, scan and output
+  kernels, one ``gdn_prefill_state_hip`` call) against bf16 MFMA peak, with
+  the algorithmic state-recurrence FLOPs; ``decode.roofline``: the decode
+  kernel against HBM peak.  Durations come from HIP events around per-phase
+  launches on the stream the kernels run on.
 * ``cpu_baseline``: the CPU oracle (oracle/, a restatement of the reference's
   PyTorch code) timed on this host on the same inputs, and the same-run parity
   of the GPU results against it.
@@ -267,12 +268,12 @@ def main():
                    "B": B, "T": T, "H": H, "dk": K, "dv": V, "chunk": C},
         "roofline": {
             "bound": "mfma",
-            "kernel": "gdn_prefill_state_kernel",
+            "kernel": "gdn_prefill_state_hip (map + scan + output kernels)",
             "achieved": state_tflops,
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": state_tflops / PEAK_BF16_TFLOPS,
-            "traffic": measured_traffic("gdn_prefill_state_kernel") if (B, T) == (1, 8192) else None,
+            "traffic": measured_traffic("prefill_state") if (B, T) == (1, 8192) else None,
             "flop_per_launch": STATE_FLOP_PER_TOKEN_HEAD * tokens * H,
             "kernel_ms": ms_state,
         },
@@ -290,7 +291,7 @@ def main():
             "dtype": "fp32",
             "roofline": {"bound": "hbm", "kernel": "gdn_decode_kernel", "achieved": dec_gbs, "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": dec_gbs / PEAK_HBM_GBS,
-                         "traffic": measured_traffic("gdn_decode_kernel"),
+                         "traffic": measured_traffic("decode"),
                          "bytes_per_launch": decode_bytes(DB, DH), "kernel_ms": ms_decode},
             "cpu_baseline": cpu_decode,
         },
