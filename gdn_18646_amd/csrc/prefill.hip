@@ -212,13 +212,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int m16 = lane & 15;
     const int g4 = lane >> 4;
 
-    // The K tile is dead after step 3; T (step 5) reuses its space.
+    // The K tile is dead after step 3: step 5 keeps the fp32 T blocks there.
     __shared__ __attribute__((aligned(16))) bf16 Kl[kC][kKLD];
     __shared__ __attribute__((aligned(16))) float Ad[kC][4][kAQ];
     __shared__ __attribute__((aligned(16))) bf16 Al[kC][kBLD];
     __shared__ float s_lg2[kC], s_bm[kC], s_ms[kC];  // s_lg2: in-chunk log2 decay cumsum
-    bf16(*const Tl)[kBLD] = reinterpret_cast<bf16(*)[kBLD]>(&Kl[0][0]);
-    static_assert(sizeof(Kl) >= sizeof(bf16) * kC * kBLD, "T tile must fit in the K tile");
+    static_assert(sizeof(Kl) >= sizeof(float) * 6 * 16 * 20, "the fp32 T blocks must fit in the K tile");
 
     int u = blockIdx.x;
     IntraUnit U = intra_unit(p, u);
@@ -331,59 +330,131 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         p.wsA[(wc * 6 + i) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
 
-    // 5) T = (I + A)^-1 by forward substitution, fp32, on all 4 waves,
-    //    right-looking: column c = 16 wave + lane/4 is owned by a quad; lane
-    //    sub = lane % 4 keeps rows i = 4q + sub (Tc[q]) and their running sums
-    //    acc[q] = sum_{j done} A[i][j] T[j][c].  Row j is final once row j-1
-    //    is folded in; its owner lane computes it, a DPP broadcast hands it to
-    //    the quad, and every lane folds it into its later rows (independent
-    //    FMAs, off the row-to-row chain).
+    // 5) T = (I + A)^-1 in fp32, blocked by 16 (block rows / columns I, J),
+    //    and Tp = T diag(beta m) in bf16 into the Aq staging tile (dead after
+    //    step 4; the upper blocks are zero):
+    //    5a each wave w inverts its diagonal block, T_ww = (I + A_ww)^-1, by
+    //       right-looking forward substitution (4 lanes per column, DPP
+    //       broadcast of each finished row);
+    //    5b T_10 = -T_11 A_10 T_00 (wave 0) and T_32 = -T_33 A_32 T_22
+    //       (wave 1), which completes T on each diagonal 32x32 half;
+    //    5c the lower left quarter, -T_hi A_hl T_lo: block (2 + r, J) goes to
+    //       wave 2J + r, which forms W_2J = A_20 T_0J + A_21 T_1J (and W_3J
+    //       for r = 1), then T_2J = -T_22 W_2J or T_3J = -(T_32 W_2J + T_33 W_3J).
+    //       What needs only diagonal blocks (all of column J = 1 but T_32 W_21,
+    //       the A_x0 T_00 terms of column 0) is done during 5b.
+    //    Products run on fp32 MFMA 16x16x4.  A first product's result, in
+    //    accumulator layout (lane l: rows 4(l/16)+i of column l%16), is the
+    //    B operand of the second product as it stands: slice i then carries
+    //    k = 4(l/16) + i, and the A operand is read in the same k order.
+    //    The diagonal blocks, T_10 and T_32 (fp32, row stride 20) live in the
+    //    dead K tile.
     {
-        int c = 16 * wave + (lane >> 2);
+        constexpr int kTS = 20;
+        float* const T32 = reinterpret_cast<float*>(&Kl[0][0]);
+        // slots: diagonal block I -> I, T_10 -> 4, T_32 -> 5
+        auto tblk = [&](int slot) { return T32 + slot * (16 * kTS); };
+        int col = lane >> 2;
         int sub = lane & 3;
-        // Opaque per unit: otherwise the compiler hoists the 64 per-row
-        // selects on c and sub out of the persistent loop and spills them.
-        asm volatile("" : "+v"(c), "+v"(sub));
-        float Tc[16], acc[16];
+        int tx = tid;
+        // Opaque per unit: otherwise the compiler hoists the per-row selects
+        // and per-thread addresses below out of the persistent loop and
+        // spills them.
+        asm volatile("" : "+v"(col), "+v"(sub), "+v"(tx));
+        const int li = tx & 15, lg = (tx >> 4) & 3;  // MFMA lane row / column, k group
+        float Tc[4];
+        {
+            float acc[4];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) Tc[q] = acc[q] = 0.f;
-        // Row j of A (this lane's slots) is loaded a row ahead into a ring;
-        // the empty asm keeps the scheduler from sinking the loads back to
-        // their use, so LDS latency overlaps the previous row's chain.
-        f32x4 ring[2][4];
-        auto load_row = [&](int j, f32x4 (&dst)[4]) {
-#pragma clang loop unroll(full)
-            for (int q4 = (j >> 2) >> 2; q4 < 4; ++q4) dst[q4] = *reinterpret_cast<const f32x4*>(&Ad[j][sub][4 * q4]);
-        };
-        load_row(0, ring[0]);
-        // Fully unrolled (the row index must be a constant: Tc stays in registers).
-#pragma clang loop unroll(full)
-        for (int j = 0; j < kC; ++j) {
-            if (j + 1 < kC) load_row(j + 1, ring[(j + 1) % 2]);
-            asm volatile("" ::: "memory");
-            const int qj = j >> 2, sj = j & 3;
-            const float own = (j == c ? 1.f : 0.f) - acc[qj];  // row j, valid in lane sub == sj
-            float tj;
-            if (sj == 0) tj = dpp_f<0x00>(own);       // quad_perm [0,0,0,0]
-            else if (sj == 1) tj = dpp_f<0x55>(own);  // quad_perm [1,1,1,1]
-            else if (sj == 2) tj = dpp_f<0xAA>(own);  // quad_perm [2,2,2,2]
-            else tj = dpp_f<0xFF>(own);               // quad_perm [3,3,3,3]
-            Tc[qj] = sub == sj ? tj : Tc[qj];
-            // Fold row j into rows i > j: slots q >= qj (slot qj only for sub > sj).
-            const f32x4(&a)[4] = ring[j % 2];
-#pragma clang loop unroll(full)
-            for (int q4 = qj >> 2; q4 < 4; ++q4) {
-#pragma clang loop unroll(full)
-                for (int u = 0; u < 4; ++u) {
-                    const int q = 4 * q4 + u;
-                    if (q > qj) acc[q] += a[q4][u] * tj;
-                    else if (q == qj && sj < 3) acc[q] += (sub > sj ? a[q4][u] : 0.f) * tj;
+            for (int q = 0; q < 4; ++q) Tc[q] = acc[q] = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int qj = j >> 2, sj = j & 3;
+                // A[16w + 4q + sub][16w + j] for q = 0..3 (this lane's rows)
+                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ad[16 * wave + j][sub][4 * wave]);
+                const float own = (j == col ? 1.f : 0.f) - acc[qj];  // row j, valid in lane sub == sj
+                float tj;
+                if (sj == 0) tj = dpp_f<0x00>(own);       // quad_perm [0,0,0,0]
+                else if (sj == 1) tj = dpp_f<0x55>(own);  // quad_perm [1,1,1,1]
+                else if (sj == 2) tj = dpp_f<0xAA>(own);  // quad_perm [2,2,2,2]
+                else tj = dpp_f<0xFF>(own);               // quad_perm [3,3,3,3]
+                Tc[qj] = sub == sj ? tj : Tc[qj];
+#pragma unroll
+                for (int q = qj; q < 4; ++q) {
+                    if (q > qj) acc[q] += a4[q] * tj;
+                    else if (sj < 3) acc[q] += (sub > sj ? a4[q] : 0.f) * tj;
                 }
             }
-        }
-        const float bmc = s_bm[c];
+            float* const tw = tblk(wave);
 #pragma unroll
-        for (int q = 0; q < 16; ++q) Tl[4 * q + sub][c] = f2bf(Tc[q] * bmc);
+            for (int q = 0; q < 4; ++q) tw[(4 * q + sub) * kTS + col] = Tc[q];
+        }
+        __syncthreads();  // diagonal blocks visible; step 4 has read Al
+
+        // acc += A_IK T_KJ, T_KJ in slot sKJ
+        auto mul_at = [&](f32x4 acc, int I, int K, int sKJ) {
+            const float* t = tblk(sKJ);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Ad[16 * K + 4 * kk + lg][li & 3][4 * I + (li >> 2)],
+                                                           t[(4 * kk + lg) * kTS + li], acc, 0, 0, 0);
+            return acc;
+        };
+        // acc += T_slot W, W in accumulator layout
+        auto mul_tw = [&](f32x4 acc, int slot, const f32x4& w) {
+            const f32x4 t4 = *reinterpret_cast<const f32x4*>(&tblk(slot)[li * kTS + 4 * lg]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(t4[i], w[i], acc, 0, 0, 0);
+            return acc;
+        };
+        // Tp block (I, J) = -x diag(beta m), x in accumulator layout
+        auto put_tp = [&](int I, int J, const f32x4& x) {
+            const float bm = -s_bm[16 * J + li];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Al[16 * I + 4 * lg + i][16 * J + li] = f2bf(x[i] * bm);
+        };
+        {
+            const float bm = s_bm[16 * wave + col];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) Al[16 * wave + 4 * q + sub][16 * wave + col] = f2bf(Tc[q] * bm);
+            // upper blocks (0,1) (0,2) (0,3) (1,2) (1,3) (2,3): waves 0, 1 two, waves 2, 3 one
+            const uint2 z = {0u, 0u};
+            for (int e = wave; e < 6; e += 4) {
+                const int I = e < 3 ? 0 : (e < 5 ? 1 : 2), J = e < 3 ? e + 1 : (e < 5 ? e - 1 : 3);
+                *reinterpret_cast<uint2*>(&Al[16 * I + col][16 * J + 4 * sub]) = z;
+            }
+        }
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 w2 = zero, w3 = zero, x = zero;
+        if (wave == 0) {
+            const f32x4 t = mul_tw(zero, 1, mul_at(zero, 1, 0, 0));
+            w2 = mul_at(zero, 2, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tblk(4)[(4 * lg + i) * kTS + li] = -t[i];
+            put_tp(1, 0, t);
+        } else if (wave == 1) {
+            const f32x4 t = mul_tw(zero, 3, mul_at(zero, 3, 2, 2));
+            w2 = mul_at(zero, 2, 0, 0);
+            w3 = mul_at(zero, 3, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tblk(5)[(4 * lg + i) * kTS + li] = -t[i];
+            put_tp(3, 2, t);
+        } else if (wave == 2) {
+            put_tp(2, 1, mul_tw(zero, 2, mul_at(zero, 2, 1, 1)));
+        } else {
+            w2 = mul_at(zero, 2, 1, 1);
+            x = mul_tw(zero, 3, mul_at(zero, 3, 1, 1));
+        }
+        __syncthreads();  // T_10, T_32 visible
+        if (wave == 0) {
+            put_tp(2, 0, mul_tw(zero, 2, mul_at(w2, 2, 1, 4)));
+        } else if (wave == 1) {
+            w2 = mul_at(w2, 2, 1, 4);
+            w3 = mul_at(w3, 3, 1, 4);
+            put_tp(3, 0, mul_tw(mul_tw(zero, 5, w2), 3, w3));
+        } else if (wave == 3) {
+            put_tp(3, 1, mul_tw(x, 5, w2));
+        }
     }
     __syncthreads();
 
@@ -391,12 +462,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
     for (int f = 2 * wave; f < 2 * wave + 2; ++f) {
         const int mt = f >> 1, s = f & 1;
-        const bf16* rp = &Tl[16 * mt + m16][32 * s + 4 * g4];
+        const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];  // Tp (step 5)
         const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
         p.wsT[(wc * 8 + f) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
-    __syncthreads();  // T (aliasing the K tile) is read before the next unit's K is stored
+    __syncthreads();  // Tp and T blocks are read before the next unit's K and Aq are stored
     u = u_next;
     U = N;
     }
