@@ -176,19 +176,22 @@ __device__ __forceinline__ IntraUnit intra_unit(const PrefillParams& p, int u) {
 
 // A unit's global inputs that are prefetched into registers: the K tile slice
 // this thread stores to LDS (rows past the sequence end zero) and wave 0's
-// gate inputs (one token per lane).
+// gate inputs (one token per lane, and A_log of the head).
 struct IntraLoads {
     u32x4 kv[4];
-    float g_m, g_a, g_b;
+    float g_m, g_alog;
+    uint32_t g_a, g_b;  // bf16 bits, widened at use (a conversion here would wait for the load)
 };
 __device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUnit& U, int tid, IntraLoads& L) {
     const int wave = tid >> 6, lane = tid & 63;
-    L.g_m = L.g_a = L.g_b = 0.f;
+    L.g_m = L.g_alog = 0.f;
+    L.g_a = L.g_b = 0u;
+    if (wave == 0) L.g_alog = p.A_log[U.h];
     if (wave == 0 && lane < U.nvalid) {
         const size_t gi = U.row_base + lane;
         L.g_m = p.mask ? p.mask[static_cast<size_t>(U.sq.b) * p.T_stride + U.sq.tok0 + U.t0 + lane] : 1.f;
-        L.g_a = bf2f(p.a[gi]);
-        L.g_b = bf2f(p.b[gi]);
+        L.g_a = p.a[gi];
+        L.g_b = p.b[gi];
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -202,6 +205,11 @@ __device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUn
 // next unit's K slice and gate inputs are loaded into registers (IntraLoads)
 // while the current unit's triangular solve runs, so global latency overlaps
 // compute.  Q (MFMA A operands of Q K^T) is read at the start of its unit.
+// All global stores of a unit (G, Aq, and the previous unit's Tp, held in
+// registers until then) are issued together after step 3: a wait for a load
+// issued while stores are in flight waits for the stores as well (the vector
+// memory counter does not order reads against writes), so the next wait,
+// at the following unit's start, finds them long complete.
 // LDS use (about 47 KiB) allows three workgroups per CU, i.e. three waves
 // per SIMD: saying so lets the scheduler spend registers on hoisting loads.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gdn_prefill_intra_kernel(
@@ -223,6 +231,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     IntraUnit U = intra_unit(p, u);
     IntraLoads L;
     if (U.valid) intra_load(p, U, tid, L);
+    u32x4 tpf[2];          // the previous unit's Tp fragments 2 wave, 2 wave + 1
+    size_t wc_prev = 0;
+    bool have_prev = false;
     while (u < p.intra_units) {
     const int u_next = u + static_cast<int>(gridDim.x);
     const IntraUnit N = intra_unit(p, u_next);
@@ -235,7 +246,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int c = U.c, h = U.h, nvalid = U.nvalid;
     const size_t wc = U.wc;
     const bool tok_ok = wave == 0 && lane < nvalid;
-    const float g_m = L.g_m, g_a = L.g_a, g_b = L.g_b;
+    const float g_m = L.g_m, g_alog = L.g_alog;
+    const float g_a = __uint_as_float(L.g_a << 16), g_b = __uint_as_float(L.g_b << 16);
     (void)c;
 
     // 1) K tile into LDS.
@@ -260,12 +272,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
 
     // 2) Gates (wave 0, one token per lane) and the in-chunk log-cumsum.
+    float G0 = 0.f, G1 = 0.f, G2 = 0.f;  // this unit's G row, stored after step 3
     if (wave == 0) {
         const int t = lane;
         float lg = 0.f, bm = 0.f, m = 0.f;
         if (tok_ok) {
             m = g_m;
-            lg = -expf(p.A_log[h]) * softplus_f(g_a + p.dt_bias);
+            lg = -expf(g_alog) * softplus_f(g_a + p.dt_bias);
             bm = sigmoid_f(g_b) * m;
         }
         const float s = wave_inclusive_sum(lg);
@@ -274,10 +287,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         s_bm[t] = bm;
         s_ms[t] = m * p.scale;
         const float gam = expf(s);
-        float* G = p.wsG + wc * 256;
-        G[t] = gam;
-        G[64 + t] = m * p.scale * gam;
-        G[128 + t] = expf(last - s);
+        G0 = gam;
+        G1 = m * p.scale * gam;
+        G2 = expf(last - s);
     }
     __syncthreads();
 
@@ -314,9 +326,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
         }
     }
+    // vmcnt(0): nothing is in flight here (every Q load was consumed above),
+    // but the compiler cannot tell on the paths that own no tile and would
+    // otherwise wait for the loads issued next before reusing Q's registers.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    // The current unit's inputs are consumed: start the next unit's loads.
+    // The current unit's inputs are consumed: start the next unit's loads,
+    // then this unit's stores.
     if (N.valid) intra_load(p, N, tid, L);
+    if (wave == 0) {
+        float* G = p.wsG + wc * 256;
+        G[lane] = G0;
+        G[64 + lane] = G1;
+        G[128 + lane] = G2;
+    }
+    if (have_prev) {
+        p.wsT[(wc_prev * 8 + 2 * wave) * 64 + lane] = tpf[0];
+        p.wsT[(wc_prev * 8 + 2 * wave + 1) * 64 + lane] = tpf[1];
+    }
 
     // 4) The six nonzero Aq fragments (mt, s) = (0,0),(1,0),(2,0),(2,1),(3,0),(3,1):
     //    lane holds Aq[16mt + m][32s + pi(g, j)].
@@ -458,18 +485,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     __syncthreads();
 
-    // 6) Tp fragments, two per wave.
+    // 6) Tp fragments, two per wave, stored with the next unit's stores.
 #pragma unroll
-    for (int f = 2 * wave; f < 2 * wave + 2; ++f) {
-        const int mt = f >> 1, s = f & 1;
+    for (int i = 0; i < 2; ++i) {
+        const int mt = wave, s = i;  // fragment f = 2 wave + i
         const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];  // Tp (step 5)
         const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
-        p.wsT[(wc * 8 + f) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        tpf[i] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
+    wc_prev = wc;
+    have_prev = true;
     __syncthreads();  // Tp and T blocks are read before the next unit's K and Aq are stored
     u = u_next;
     U = N;
+    }
+    if (have_prev) {
+        p.wsT[(wc_prev * 8 + 2 * wave) * 64 + lane] = tpf[0];
+        p.wsT[(wc_prev * 8 + 2 * wave + 1) * 64 + lane] = tpf[1];
     }
 }
 
