@@ -138,7 +138,12 @@ __device__ __forceinline__ float wave_inclusive_sum(float v) {
 }
 
 constexpr int kKLD = kDK + 8;  // padded LDS row (bf16) for K and Q tiles
-constexpr int kAQ = kC / 4 + 4;  // A stored by column, de-interleaved: Ad[j][i % 4][i / 4], padded
+// A is stored by column, de-interleaved: element (i, j) at Ad[j][(i % 4) kAQ + i / 4].
+// Rows of 16 + 4 floats keep the 4-row reads 16-byte aligned; the extra 4
+// floats per column make the column stride 84 floats, so the 64 lanes of a
+// step-3 write (16 columns x 4 row groups) hit 64 different banks.
+constexpr int kAQ = kC / 4 + 4;
+constexpr int kADS = 4 * kAQ + 4;
 constexpr int kBLD = kC + 8;   // padded LDS row (bf16) for 64x64 tiles
 
 // One (chunk, sequence-head) unit of kernel 1.  Unit u maps to head, chunk
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
     // The K tile is dead after step 3: step 5 keeps the fp32 T blocks there.
     __shared__ __attribute__((aligned(16))) bf16 Kl[kC][kKLD];
-    __shared__ __attribute__((aligned(16))) float Ad[kC][4][kAQ];
+    __shared__ __attribute__((aligned(16))) float Ad[kC][kADS];
     __shared__ __attribute__((aligned(16))) bf16 Al[kC][kBLD];
     __shared__ float s_lg2[kC], s_bm[kC], s_ms[kC];  // s_lg2: in-chunk log2 decay cumsum
     static_assert(sizeof(Kl) >= sizeof(float) * 6 * 16 * 20, "the fp32 T blocks must fit in the K tile");
@@ -322,7 +327,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * ti + 4 * g4 + i;
             const float d = __builtin_amdgcn_exp2f(s_lg2[row] - lg2_col);  // Gamma_{row,col}
-            Ad[col][row & 3][row >> 2] = row > col ? s_bm[row] * accK[i] * d : 0.f;
+            Ad[col][(row & 3) * kAQ + (row >> 2)] = row > col ? s_bm[row] * accK[i] * d : 0.f;
             Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
         }
     }
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             for (int j = 0; j < 16; ++j) {
                 const int qj = j >> 2, sj = j & 3;
                 // A[16w + 4q + sub][16w + j] for q = 0..3 (this lane's rows)
-                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ad[16 * wave + j][sub][4 * wave]);
+                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ad[16 * wave + j][sub * kAQ + 4 * wave]);
                 const float own = (j == col ? 1.f : 0.f) - acc[qj];  // row j, valid in lane sub == sj
                 float tj;
                 if (sj == 0) tj = dpp_f<0x00>(own);       // quad_perm [0,0,0,0]
@@ -418,13 +423,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         }
         __syncthreads();  // diagonal blocks visible; step 4 has read Al
 
-        // acc += A_IK T_KJ, T_KJ in slot sKJ
+        // acc += A_IK T_KJ, T_KJ in slot sKJ.  Slice kk, lane group lg carries
+        // k = 4 lg + kk: the 64 lanes' A reads then fall in 64 banks.
         auto mul_at = [&](f32x4 acc, int I, int K, int sKJ) {
             const float* t = tblk(sKJ);
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Ad[16 * K + 4 * kk + lg][li & 3][4 * I + (li >> 2)],
-                                                           t[(4 * kk + lg) * kTS + li], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Ad[16 * K + 4 * lg + kk][(li & 3) * kAQ + 4 * I + (li >> 2)],
+                                                           t[(4 * lg + kk) * kTS + li], acc, 0, 0, 0);
             return acc;
         };
         // acc += T_slot W, W in accumulator layout
