@@ -734,8 +734,11 @@ __device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const
 // the MFMA chain that does depend on it rarely waits on LDS, without holding
 // every fragment in registers at once.  `v_zero`: the tile has no V (identity
 // columns of the map pass).  `next` issues the following chunk's copies.
-template <int MODE, int NW, int NT>
-__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
+// LATE_Q: P = Q S is formed after dV instead of with K S, so that the two
+// waves sharing a SIMD (waves w and w + 4) read the staged fragments at
+// different times instead of all waves loading K and Q at once.
+template <int MODE, int NW, int NT, bool LATE_Q>
+__device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
                                             int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
                                             const Stager<MODE, NW, NT>& next) {
     using St = Stage<MODE, NW, NT>;
@@ -745,7 +748,7 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 
     next.issue();
 
-    // (a) X = K S (and P = Q S for the output), in two k-halves so only half
+    // (a) X = K S (and P = Q S for the output unless LATE_Q), in two k-halves so only half
     //     of the K and Q fragments is held at a time.
     f32x4 X[4][NT], P[4][NT];
 #pragma unroll
@@ -761,7 +764,7 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
             for (int s2 = 0; s2 < 2; ++s2) {
                 const int f = 4 * mt + 2 * half + s2;
                 kf[mt][s2] = kfrag(buf + St::offK, f, lane);
-                if constexpr (St::out) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
+                if constexpr (St::out && !LATE_Q) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
             }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
@@ -774,7 +777,7 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     X[mt][nt] = mfma16x16x32(kf[mt][s2], Bs[nt], X[mt][nt]);
-                    if constexpr (St::out) P[mt][nt] = mfma16x16x32(qf[mt][s2], Bs[nt], P[mt][nt]);
+                    if constexpr (St::out && !LATE_Q) P[mt][nt] = mfma16x16x32(qf[mt][s2], Bs[nt], P[mt][nt]);
                 }
         }
     }
@@ -848,6 +851,20 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
         BS0[nt] = pack8(kd[0] * D[0][nt], kd[1] * D[1][nt]);
         BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
     }
+    if constexpr (St::out && LATE_Q) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            bf16x8 Bs[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const bf16x8 q = frag(buf, St::offQ + (4 * mt + s) * kFragB, lane);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) P[mt][nt] = mfma16x16x32(q, Bs[nt], P[mt][nt]);
+            }
+        }
+    }
     if constexpr (!kEarlyKt) load_kt();
     // (e) S <- gamma_C S + K^T (decay o dV)  (issued before (d): the recurrence's critical path).
 #pragma unroll
@@ -900,6 +917,16 @@ __device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT]
             if (row < nvalid) *reinterpret_cast<u32x4*>(ob + row * dv + col0_wave + 8 * q) = v;
         }
     }
+}
+
+template <int MODE, int NW, int NT>
+__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
+                                            int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
+                                            const Stager<MODE, NW, NT>& next) {
+    if (MODE == kModeOut && NW == 8 && wave >= 4)
+        state_chunk_impl<MODE, NW, NT, true>(buf, S, ob, dv, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
+    else
+        state_chunk_impl<MODE, NW, NT, false>(buf, S, ob, dv, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
 }
 
 // Work decomposition of the state pass.
