@@ -1107,10 +1107,13 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 // MFMA k-step s, so wave w publishes its rows as one 8-byte half of k-step
 // w / 2's B operand (bf16 high and low parts of the fp32 state, which give
 // two independent accumulation chains) and every wave reads all four k-steps
-// back.  Each wave copies its own phi fragments and psi quad into an LDS ring
-// kScanRing - 1 steps ahead (asynchronous copies, explicit wait counts).
-constexpr int kScanRing = 3;
-constexpr int kScanSlot = 5 * kFragB;  // per wave and step: 4 phi fragments, 1 psi quad
+// back.  The steps are a dependent chain, so what bounds a step is latency:
+// each wave holds its phi fragments and psi quad for the next kScanDepth
+// steps in registers (20 VGPRs a step), loaded kScanDepth steps before use,
+// which covers the memory latency that a shallower LDS ring (limited to 3
+// steps by LDS capacity) did not.
+constexpr int kScanDepth = 6;
+constexpr int kMaxGroups = 16;  // chunk groups per sequence (plan_state caps G here)
 
 __device__ __forceinline__ u32x2 pack4_hi(const f32x4 v) {
     u32x2 r;
@@ -1128,12 +1131,16 @@ __device__ __forceinline__ u32x2 pack4_lo(const f32x4 v, const u32x2 hi) {
     return pack4_hi(d);
 }
 
+// STEPS = G - 1 is a template parameter so that the step loop unrolls
+// completely with static register slots and exact wait counts (a rolled
+// loop makes the compiler wait for every outstanding load at its header).
+template <int STEPS>
 __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, StateGrid sg) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * 8 * kFragB + kScanRing * 8 * kScanSlot];
+    static_assert(STEPS >= 1 && STEPS < kMaxGroups, "scan steps");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * 8 * kFragB];
     const int dv = p.dv, ntile = dv / 16;
     const int nunits = sg.nheads * ntile;
-    const int steps = sg.ngroups - 1;
-    if (static_cast<int>(blockIdx.x) >= nunits || steps <= 0) return;  // uniform over the workgroup
+    if (static_cast<int>(blockIdx.x) >= nunits) return;  // uniform over the workgroup
     int head, tile;
     if (p.xcd_heads) {
         const HeadItem hi = head_major_xcd(blockIdx.x, ntile);
@@ -1149,7 +1156,6 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
     const int n = lane & 15, g = lane >> 4;
     const int col = 16 * tile + n;
     lds_u8* const sbuf = (lds_u8*)&smem[0];
-    lds_u8* const ring = (lds_u8*)&smem[2 * 8 * kFragB] + wave * kScanSlot;
 
     f32x4 S;
     if (p.state_in) {
@@ -1160,26 +1166,27 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
         S = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     auto psi_at = [&](int j) {
-        return sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048;
+        return reinterpret_cast<f32x4*>(sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048) +
+               wave * 64 + lane;
     };
     // This wave's phi fragments (row tile r, k-steps 0..3: 4 contiguous KiB)
-    // and psi quad r (1 KiB); every copy reads 1 KiB, 16 bytes a lane.
-    const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
-    auto stage = [&](int j, int slot) {  // 5 copies per wave
-        const unsigned char* ph = reinterpret_cast<const unsigned char*>(
-            sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) + 4 * wave * kFragB;
-        lds_u8* dst = ring + slot * 8 * kScanSlot;
+    // and psi quad r of step j, into register slot j % kScanDepth.
+    constexpr int D = STEPS < kScanDepth ? STEPS : kScanDepth;
+    u32x4 ph[D][4];
+    f32x4 ps[D];
+    auto load = [&](int j) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) +
+                           4 * wave * 64 + lane;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) dma16(ph + ks * kFragB, lane16, dst + ks * kFragB);
-        dma16(reinterpret_cast<const unsigned char*>(psi_at(j)) + wave * kFragB, lane16, dst + 4 * kFragB);
+        for (int ks = 0; ks < 4; ++ks) ph[j % D][ks] = src[ks * 64];
+        ps[j % D] = *psi_at(j);
+        // Keep each step's loads together and in step order: the wait for
+        // step j then only covers what was issued up to step j.
+        __builtin_amdgcn_sched_barrier(0);
     };
-    // Every step issues one stage (clamped to the last step), so the copy for
-    // step j always has exactly 1 (store) + 5 + 1 operations after it when
-    // step j begins, for kScanRing = 3.  A step's stage is issued right after
-    // its MFMAs, so copy issue overlaps their latency instead of preceding them.
-    static_assert(kScanRing == 3, "wait count below assumes a 3-deep ring");
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int d = 0; d < kScanRing - 1; ++d) stage(min(d, steps - 1), d);
+    for (int j = 0; j < D; ++j) load(j);
     const int half = (wave & 1) * 8;  // this row tile's bytes in its k-step's B fragment
     auto publish = [&](lds_u8* buf) {
         const u32x2 hi = pack4_hi(S);
@@ -1187,29 +1194,36 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
         *reinterpret_cast<lds_u32x2*>(buf + (2 * (wave >> 1) + 1) * kFragB + 16 * lane + half) = pack4_lo(S, hi);
     };
     publish(sbuf);
-    for (int j = 0; j < steps; ++j) {
-        const int slot = j % kScanRing;
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
         lds_u8* const buf = sbuf + (j & 1) * 8 * kFragB;
-        if (j == 0)
-            wait_vm<5>();  // the first stage; the second may still be in flight
-        else
-            wait_vm<7>();
         lds_barrier();
-        const lds_u8* src = ring + slot * 8 * kScanSlot;
-        f32x4 acc_h = *reinterpret_cast<const lds_f32x4*>(src + 4 * kFragB + 16 * lane);
+        f32x4 acc_h = ps[j % D];
         f32x4 acc_l = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const bf16x8 a = frag(src, ks * kFragB, lane);
+            const bf16x8 a = as_bf16x8(ph[j % D][ks]);
             acc_h = mfma16x16x32(a, frag(buf, (2 * ks) * kFragB, lane), acc_h);
             acc_l = mfma16x16x32(a, frag(buf, (2 * ks + 1) * kFragB, lane), acc_l);
         }
-        stage(min(j + kScanRing - 1, steps - 1), (j + kScanRing - 1) % kScanRing);
+        if (j + D < STEPS) load(j + D);
         S = acc_h + acc_l;
-        reinterpret_cast<f32x4*>(psi_at(j))[wave * 64 + lane] = S;
+        *psi_at(j) = S;
         publish(sbuf + ((j + 1) & 1) * 8 * kFragB);
     }
-    wait_vm<0>();  // the clamped trailing copies land before the workgroup's LDS is released
+}
+
+template <int STEPS>
+int launch_scan(const PrefillParams& p, const StateGrid& sg, unsigned nblocks, hipStream_t stream, int steps) {
+    if constexpr (STEPS < kMaxGroups) {
+        if (steps == STEPS) {
+            hipLaunchKernelGGL((gdn_prefill_scan_kernel<STEPS>), dim3(nblocks), dim3(512), 0, stream, p, sg);
+            return gdn_host::check_launch("gdn_prefill_scan_kernel");
+        }
+        return launch_scan<STEPS + 1>(p, sg, nblocks, stream, steps);
+    } else {
+        return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: %d chunk groups", steps + 1);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1273,7 +1287,8 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
     }
     const long long base = nheads * s.nvg_out;  // output-pass workgroups with one group
     long long G = 1;
-    if (base < 256 && max_chunks >= 8) G = std::min<long long>(std::min<long long>(16, 256 / base), max_chunks / 4);
+    if (base < 256 && max_chunks >= 8)
+        G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
     if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
     s.G = G < 2 ? 1 : static_cast<int>(G);
     return s;
@@ -1383,8 +1398,7 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
         if (st != GDN_OK) return st;
         const long long nscan = nheads * (p.dv / 16);
         if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-        hipLaunchKernelGGL(gdn_prefill_scan_kernel, dim3(static_cast<unsigned>(nscan)), dim3(512), 0, stream, p, sg);
-        st = gdn_host::check_launch("gdn_prefill_scan_kernel");
+        st = launch_scan<1>(p, sg, static_cast<unsigned>(nscan), stream, sp.G - 1);
         if (st != GDN_OK) return st;
     }
     sg.nvg = sp.nvg_out;
