@@ -17,8 +17,11 @@ with the achieved MFMA / HBM roofline fractions.
 * ``cpu_baseline``: the CPU oracle (oracle/, a restatement of the reference's
   PyTorch code) timed on this host on the same inputs, and the same-run parity
   of the GPU results against it.
+* ``prefill_batches``: the same prefill at B=4 and B=8; ``layer_e2e``: the
+  end-to-end layer of config 5 (RMSNorm, fused projection + conv + SiLU,
+  prefill, output projection at B=4 x T=4096, then decode steps at B=4).
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-extra]
 """
 
 import argparse
@@ -96,6 +99,8 @@ def main():
     ap.add_argument("--T", type=int, default=8192)
     ap.add_argument("--B", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the B=4/8 prefill lines and the end-to-end layer (config 5) timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device copies of exactly 256 MiB (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -163,6 +168,25 @@ def main():
         f"intra {ms_intra:.4f} ms ({intra_tflops:.1f} TF/s), state {ms_state:.4f} ms ({state_tflops:.1f} TF/s); "
         f"path {path_tflops:.1f} TF/s, {path_gbs:.0f} GB/s")
 
+    # ------------------------------------------------------------ prefill, B = 4 and 8
+    batches = {}
+    if not args.no_extra:
+        for Bx in (4, 8):
+            dx = synth.prefill_inputs(Bx, T, H, K, V, seed=1)
+            gx = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in dx.items()}
+
+            def step_x():
+                return pf.prefill(gx["q"], gx["k"], gx["v"], gx["A_log"], gx["a"], 0.0, gx["b_logits"], gx["mask"],
+                                  empty, 0.0)
+
+            for _ in range(2):
+                step_x()
+            msx = time_events(step_x, max(3, args.steps // 2), torch)
+            batches[f"B{Bx}"] = {"ms": msx, "tokens_per_s": Bx * T / (msx / 1e3),
+                                 "path_tflops": PREFILL_FLOP_PER_TOKEN_HEAD * Bx * T * H / (msx / 1e3) / 1e12}
+            log(f"prefill B={Bx} T={T} H={H}: {msx:.4f} ms/step, {Bx * T / (msx / 1e3):.4g} tok/s")
+            del dx, gx
+
     # ------------------------------------------------------------------ decode
     DB, DH = 256, 32
     dd = synth.decode_inputs(DB, DH, K, V, seed=2)
@@ -194,6 +218,36 @@ def main():
     ms_decode = time_events(decode_step, args.decode_steps, torch)
     dec_gbs = decode_bytes(DB, DH) / (ms_decode / 1e3) / 1e9
     log(f"decode B={DB} H={DH}: {ms_decode * 1e3:.1f} us/step, {1e3 / ms_decode:.1f} steps/s, {dec_gbs:.0f} GB/s")
+
+    # ------------------------------------------------- end-to-end layer (config 5)
+    layer_e2e = None
+    if not args.no_extra:
+        from gdn_18646_amd.gdn_layer import GDNLayerCustom, make_weights
+
+        gl = torch.Generator().manual_seed(5)
+        wl = {k: v.to(dev) for k, v in make_weights(device="cpu", D=2048, H=16, DK=128, DV=128, std=0.02,
+                                                     generator=gl).items()}
+        layer = GDNLayerCustom(wl, exts)
+        LB, LT = 4, 4096
+        xl = torch.randn(LB, LT, 2048, generator=gl).bfloat16().to(dev)
+        xd = [torch.randn(LB, 1, 2048, generator=gl).bfloat16().to(dev) for _ in range(8)]
+        _, st_l = layer.forward(xl, return_state=True)
+        ms_lf = time_events(lambda: layer.forward(xl), max(3, args.steps // 4), torch)
+        it_l = iter(range(10 ** 9))
+
+        def layer_dec():
+            layer.decode(xd[next(it_l) % len(xd)], st_l, inplace=True)
+
+        for _ in range(3):
+            layer_dec()
+        ms_ld = time_events(layer_dec, 128, torch)
+        layer_e2e = {"config": "hidden 2048, H=16, dk=dv=128, conv 4, weights N(0, 0.02); prefill B=4 x T=4096, "
+                               "then decode steps at B=4 continuing from the prefill state",
+                     "prefill_ms": ms_lf, "prefill_tokens_per_s": LB * LT / (ms_lf / 1e3),
+                     "decode_ms_per_step": ms_ld, "decode_steps_per_s": 1e3 / ms_ld}
+        log(f"layer (config 5): prefill B={LB} T={LT} {ms_lf:.3f} ms ({LB * LT / (ms_lf / 1e3):.4g} tok/s), "
+            f"decode B={LB} {ms_ld * 1e3:.1f} us/step")
+        del layer, wl, xl, st_l
 
     # ------------------------------------------------------------------ CPU oracle
     cpu_prefill = cpu_decode = None
@@ -284,6 +338,8 @@ def main():
             "path_gbs": path_gbs, "path_hbm_frac": path_gbs / PEAK_HBM_GBS,
             "path_flop": PREFILL_FLOP_PER_TOKEN_HEAD * tokens * H, "path_bytes": prefill_bytes(B, T, H),
         },
+        "prefill_batches": batches or None,
+        "layer_e2e": layer_e2e,
         "decode": {
             "value": 1e3 / ms_decode, "unit": "steps/s", "ms_per_step": ms_decode, "steps": args.decode_steps,
             "config": {"workload": "GDN decode B=256 H=32 dk=dv=128, fp32 state in place, fresh q/k/v each step",
