@@ -534,7 +534,7 @@ struct Stage {
     static constexpr int offV = offG + kFragB;
     static constexpr int vWave = 2 * NT * kFragB;
     static constexpr int bytes = offV + NW * vWave;
-    static constexpr int stores = out ? 2 * NT : 0;                 // output stores per chunk per wave
+    static constexpr int stores = out ? 4 * NT : 0;                 // output stores per chunk per wave
 };
 
 
@@ -623,31 +623,32 @@ struct Stager {
         const int m = lane & 15, g = lane >> 4;
         const unsigned char* kb = reinterpret_cast<const unsigned char*>(p->k + row_base * kDK);
         const unsigned char* qb = reinterpret_cast<const unsigned char*>(p->q + row_base * kDK);
-#pragma unroll
-        for (int f = 0; f < NJ; ++f) {
-            if (f % NW != wave) continue;  // uniform
+        // The shared jobs are staged contiguously in job order (K, Q, Tp, Aq,
+        // gate block), so job f lands at f KiB.  Each wave walks only its own
+        // jobs f = wave, wave + NW, ... (a uniform loop).
+        static_assert(St::offK == 0 && St::offQ == nK * kFragB && St::offT == (nK + nQ) * kFragB &&
+                          St::offG == (nK + nQ + nT + nA) * kFragB && (!St::out || St::offA == St::offT + nT * kFragB),
+                      "staging layout must follow job order");
+        for (int f = wave; f < NJ; f += NW) {
+            lds_u8* const dst = buf + f * kFragB;
             if (f < nK + nQ) {
                 const bool isq = f >= nK;
                 const int ff = isq ? f - nK : f;
                 const unsigned char* base = isq ? qb : kb;
                 if (full) {
-                    dma16(base + (ff >> 2) * 16 * kDK * 2 + (ff & 3) * 64, isq ? L->q : L->k,
-                          buf + (isq ? St::offQ : St::offK) + ff * kFragB);
+                    dma16(base + (ff >> 2) * 16 * kDK * 2 + (ff & 3) * 64, isq ? L->q : L->k, dst);
                 } else {
                     const int row = min(16 * (ff >> 2) + (isq ? m : kslot_row(lane)), nvalid - 1);
-                    dma16(base, static_cast<uint32_t>((row * kDK + 32 * (ff & 3) + 8 * g) * 2),
-                          buf + (isq ? St::offQ : St::offK) + ff * kFragB);
+                    dma16(base, static_cast<uint32_t>((row * kDK + 32 * (ff & 3) + 8 * g) * 2), dst);
                 }
             } else if (f < nK + nQ + nT) {
-                const int ff = f - nK - nQ;
-                dma16(reinterpret_cast<const unsigned char*>(p->wsT + wc * 8 * 64) + ff * kFragB, L->fr,
-                      buf + St::offT + ff * kFragB);
+                dma16(reinterpret_cast<const unsigned char*>(p->wsT + wc * 8 * 64) + (f - nK - nQ) * kFragB, L->fr,
+                      dst);
             } else if (f < nK + nQ + nT + nA) {
-                const int ff = f - nK - nQ - nT;
-                dma16(reinterpret_cast<const unsigned char*>(p->wsA + wc * 6 * 64) + ff * kFragB, L->fr,
-                      buf + St::offA + ff * kFragB);
+                dma16(reinterpret_cast<const unsigned char*>(p->wsA + wc * 6 * 64) + (f - nK - nQ - nT) * kFragB,
+                      L->fr, dst);
             } else {
-                dma16(p->wsG + wc * 256, L->fr, buf + St::offG);
+                dma16(p->wsG + wc * 256, L->fr, dst);
             }
         }
         if (v_on) {
@@ -728,6 +729,14 @@ __device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const
     return r;
 }
 
+// Four floats -> four bf16 (round to nearest even), as 8 bytes.
+__device__ __forceinline__ u32x2 pack4_bf16(const f32x4 v) {
+    u32x2 r;
+    r[0] = static_cast<uint32_t>(f2bf_bits(v[0])) | (static_cast<uint32_t>(f2bf_bits(v[1])) << 16);
+    r[1] = static_cast<uint32_t>(f2bf_bits(v[2])) | (static_cast<uint32_t>(f2bf_bits(v[3])) << 16);
+    return r;
+}
+
 // One chunk of the state recurrence for a 128 x (16 NT) column tile, operands
 // in LDS.  `ob` points at out[row_base][0] (uniform).  Operand fragments are
 // read from LDS one phase ahead of their use (none depends on the state), so
@@ -777,7 +786,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     X[mt][nt] = mfma16x16x32(kf[mt][s2], Bs[nt], X[mt][nt]);
-                    if constexpr (St::out && !LATE_Q) P[mt][nt] = mfma16x16x32(qf[mt][s2], Bs[nt], P[mt][nt]);
+                    if constexpr (St::out && !LATE_Q) P[mt][nt] = mfma16x16x32(Bs[nt], qf[mt][s2], P[mt][nt]);
                 }
         }
     }
@@ -861,7 +870,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
             for (int mt = 0; mt < 4; ++mt) {
                 const bf16x8 q = frag(buf, St::offQ + (4 * mt + s) * kFragB, lane);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) P[mt][nt] = mfma16x16x32(q, Bs[nt], P[mt][nt]);
+                for (int nt = 0; nt < NT; ++nt) P[mt][nt] = mfma16x16x32(Bs[nt], q, P[mt][nt]);
             }
         }
     }
@@ -882,39 +891,28 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
             BD0[nt] = pack8(D[0][nt], D[1][nt]);
             BD1[nt] = pack8(D[2][nt], D[3][nt]);
         }
-        // (d) O = (m scale gamma) o P + Aq dV -> bf16, staged through this
-        //     wave's V area (free once V is in registers) so each row leaves
-        //     as 16-byte pieces: 2 NT stores per wave instead of 16 NT.  The
-        //     staged rows have their 16-byte pieces XOR-swizzled by row / 4 so
-        //     the 2-byte writes of the four lane groups hit different banks.
-        f32x4 co[4];
+        // (d) O^T = (m scale gamma) o P^T + dV^T Aq^T, formed transposed so
+        //     each lane holds 4 consecutive output columns of one token: the
+        //     dV packs are the A operands and the Aq fragments the B operands
+        //     as they stand (both carry their k in pi order), and P^T = S^T Q^T
+        //     was accumulated with the operands of Q S swapped.  Lane (n, g) of
+        //     tile mt stores out[token 16 mt + n][16 nt + 4 g .. + 3] as 8 bytes.
+        float co[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) co[mt] = *reinterpret_cast<const lds_f32x4*>(G + 64 + 16 * mt + 4 * g);
-        constexpr int kRowB = 32 * NT;          // staged row: 16 NT bf16
-        constexpr int kPieces = 2 * NT;         // 16-byte pieces per row
-        lds_u8* ot = const_cast<lds_u8*>(buf) + St::offV + wave * St::vWave;
+        for (int mt = 0; mt < 4; ++mt) co[mt] = G[64 + 16 * mt + n];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             f32x4 O[4];
-            O[0] = mfma16x16x32(af[0], BD0[nt], co[0] * P[0][nt]);
-            O[1] = mfma16x16x32(af[1], BD0[nt], co[1] * P[1][nt]);
-            O[2] = mfma16x16x32(af[3], BD1[nt], mfma16x16x32(af[2], BD0[nt], co[2] * P[2][nt]));
-            O[3] = mfma16x16x32(af[5], BD1[nt], mfma16x16x32(af[4], BD0[nt], co[3] * P[3][nt]));
-            const int col = 16 * nt + n;
+            O[0] = mfma16x16x32(BD0[nt], af[0], co[0] * P[0][nt]);
+            O[1] = mfma16x16x32(BD0[nt], af[1], co[1] * P[1][nt]);
+            O[2] = mfma16x16x32(BD1[nt], af[3], mfma16x16x32(BD0[nt], af[2], co[2] * P[2][nt]));
+            O[3] = mfma16x16x32(BD1[nt], af[5], mfma16x16x32(BD0[nt], af[4], co[3] * P[3][nt]));
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = 16 * mt + 4 * g + i;
-                    const int piece = (col >> 3) ^ ((row >> 2) & (kPieces - 1));
-                    *reinterpret_cast<lds_u16*>(ot + row * kRowB + piece * 16 + (col & 7) * 2) = f2bf_bits(O[mt][i]);
-                }
-        }
-#pragma unroll
-        for (int k = 0; k < kPieces; ++k) {
-            const int idx = 64 * k + lane, row = idx / kPieces, q = idx % kPieces;
-            const u32x4 v = *reinterpret_cast<const lds_u32x4*>(ot + row * kRowB + (q ^ ((row >> 2) & (kPieces - 1))) * 16);
-            if (row < nvalid) *reinterpret_cast<u32x4*>(ob + row * dv + col0_wave + 8 * q) = v;
+            for (int mt = 0; mt < 4; ++mt) {
+                const int row = 16 * mt + n;
+                if (row < nvalid)
+                    *reinterpret_cast<u32x2*>(ob + row * dv + col0_wave + 16 * nt + 4 * g) = pack4_bf16(O[mt]);
+            }
         }
     }
 }
