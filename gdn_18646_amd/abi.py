@@ -25,6 +25,8 @@ SIGNATURES = {
     "gdn_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "gdn_prefill_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,
                              _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "gdn_prefill_tm_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,
+                                _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "gdn_prefill_intra_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,
                                    _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "gdn_prefill_state_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,

@@ -55,7 +55,7 @@ gdn_bf16_t* bf_mut(const Tensor& t) { return reinterpret_cast<gdn_bf16_t*>(t.dat
 // prefill
 // ---------------------------------------------------------------------------
 std::tuple<Tensor, Tensor> prefill(Tensor q, Tensor k, Tensor v, Tensor A_log, Tensor a, double dt_bias,
-                                   Tensor b_logits, Tensor mask, Tensor state_in, double scale) {
+                                   Tensor b_logits, Tensor mask, Tensor state_in, double scale, bool token_major) {
     check_bf16(q, "q");
     check_bf16(k, "k");
     check_bf16(v, "v");
@@ -84,14 +84,14 @@ std::tuple<Tensor, Tensor> prefill(Tensor q, Tensor k, Tensor v, Tensor A_log, T
         sin_ptr = state_in.data_ptr<float>();
     }
     const c10::DeviceGuard guard(q.device());
-    auto out = at::empty({B, H, T, V}, q.options());
+    auto out = token_major ? at::empty({B, T, H, V}, q.options()) : at::empty({B, H, T, V}, q.options());
     auto state_out = at::empty({B, H, K, V}, q.options().dtype(at::kFloat));
     const size_t ws_bytes = gdn_prefill_workspace_bytes(B, H, T, K, V);
     auto ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
-    GDN_CHECK_STATUS(gdn_prefill_hip(bf(q), bf(k), bf(v), A_log.data_ptr<float>(), bf(a), static_cast<float>(dt_bias),
-                                     bf(b_logits), mask_ptr, sin_ptr, static_cast<float>(scale), bf_mut(out),
-                                     state_out.data_ptr<float>(), B, H, T, K, V, ws.data_ptr(), ws_bytes,
-                                     stream_of(q)),
+    auto fn = token_major ? &gdn_prefill_tm_hip : &gdn_prefill_hip;
+    GDN_CHECK_STATUS(fn(bf(q), bf(k), bf(v), A_log.data_ptr<float>(), bf(a), static_cast<float>(dt_bias),
+                        bf(b_logits), mask_ptr, sin_ptr, static_cast<float>(scale), bf_mut(out),
+                        state_out.data_ptr<float>(), B, H, T, K, V, ws.data_ptr(), ws_bytes, stream_of(q)),
                      "prefill");
     return {out, state_out};
 }
@@ -315,9 +315,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     mp.def("prefill", &prefill,
            "Args: q,k [B,H,T,K] bf16 | v [B,H,T,V] bf16 | A_log [H] fp32 | a,b_logits [B,H,T] bf16 | "
            "dt_bias float | mask [B,T] fp32 (empty = ones) | state_in [B,H,K,V] fp32 (empty = zeros) | "
-           "scale float (0 = K^-0.5)\nReturns: (out [B,H,T,V] bf16, state_out [B,H,K,V] fp32)",
+           "scale float (0 = K^-0.5) | token_major (keyword, default False)\n"
+           "Returns: (out [B,H,T,V] bf16, or [B,T,H,V] with token_major, state_out [B,H,K,V] fp32)",
            py::arg("q"), py::arg("k"), py::arg("v"), py::arg("A_log"), py::arg("a"), py::arg("dt_bias"),
-           py::arg("b_logits"), py::arg("mask"), py::arg("state_in"), py::arg("scale"));
+           py::arg("b_logits"), py::arg("mask"), py::arg("state_in"), py::arg("scale"), py::kw_only(),
+           py::arg("token_major") = false);
     mp.def("prefill_varlen", &prefill_varlen,
            "Packed varlen prefill: q,k [1,H,Ttot,K] | v [1,H,Ttot,V] | a,b_logits [1,H,Ttot] | cu_seqlens [N+1] | "
            "state_in [N,H,K,V] or empty.  Returns (out [1,H,Ttot,V] bf16, state_out [N,H,K,V] fp32)",

@@ -71,6 +71,7 @@ struct PrefillParams {
     int T_len;           // batch mode: sequence length
     int chunks_per_seq;  // batch mode: ceil(T_len / 64)
     int xcd_heads;       // (sequence, head) pairs are a multiple of 8: head-aligned XCD mapping
+    int out_tm;          // out is token-major ([B, T, H, dv] / [T_total, H, dv]) instead of head-major
     int nchunk_grid;     // intra kernel: chunks per (sequence, head) in the grid
     int intra_units;     // intra kernel: (sequence, head) pairs x nchunk_grid
 };
@@ -747,7 +748,7 @@ __device__ __forceinline__ u32x2 pack4_bf16(const f32x4 v) {
 // waves sharing a SIMD (waves w and w + 4) read the staged fragments at
 // different times instead of all waves loading K and Q at once.
 template <int MODE, int NW, int NT, bool LATE_Q>
-__device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
+__device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int orow, int nvalid,
                                             int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
                                             const Stager<MODE, NW, NT>& next) {
     using St = Stage<MODE, NW, NT>;
@@ -911,20 +912,20 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
             for (int mt = 0; mt < 4; ++mt) {
                 const int row = 16 * mt + n;
                 if (row < nvalid)
-                    *reinterpret_cast<u32x2*>(ob + row * dv + col0_wave + 16 * nt + 4 * g) = pack4_bf16(O[mt]);
+                    *reinterpret_cast<u32x2*>(ob + row * orow + col0_wave + 16 * nt + 4 * g) = pack4_bf16(O[mt]);
             }
         }
     }
 }
 
 template <int MODE, int NW, int NT>
-__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int dv, int nvalid,
+__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int orow, int nvalid,
                                             int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
                                             const Stager<MODE, NW, NT>& next) {
     if (MODE == kModeOut && NW == 8 && wave >= 4)
-        state_chunk_impl<MODE, NW, NT, true>(buf, S, ob, dv, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
+        state_chunk_impl<MODE, NW, NT, true>(buf, S, ob, orow, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
     else
-        state_chunk_impl<MODE, NW, NT, false>(buf, S, ob, dv, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
+        state_chunk_impl<MODE, NW, NT, false>(buf, S, ob, orow, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
 }
 
 // Work decomposition of the state pass.
@@ -1028,6 +1029,13 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 
     const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
     auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
+    // Output rows: head-major out[(sequence, head)][token][dv], or token-major
+    // out[sequence][token][head][dv] (row stride H dv), as the caller asked.
+    const int orow = p.out_tm ? p.H * dv : dv;
+    auto obase = [&](int c) {
+        const size_t tok = static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + static_cast<size_t>(c) * kC;
+        return p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv;
+    };
     auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
     auto wcof = [&](int c) { return static_cast<size_t>(sq.slot0 + c) * p.H + h; };
     auto step = [&](int c, lds_u8* cur, lds_u8* nxt) {
@@ -1044,7 +1052,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
             zero_pad_rows<MODE, NW, NT>(cur, nv, wave, lane);
             lds_barrier();
         }
-        state_chunk<MODE, NW, NT>(cur, S, p.out + rows(c) * dv, dv, nv, wave, lane, col0_wave, phi_cols, kt_lane,
+        state_chunk<MODE, NW, NT>(cur, S, p.out + obase(c), orow, nv, wave, lane, col0_wave, phi_cols, kt_lane,
                                   next);
     };
 
@@ -1434,7 +1442,8 @@ namespace {
 int prefill_batch(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
                   const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
                   const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H, int T,
-                  int dk, int dv, void* workspace, size_t workspace_bytes, void* stream, int phases) {
+                  int dk, int dv, void* workspace, size_t workspace_bytes, void* stream, int phases,
+                  int out_tm = 0) {
     using gdn_host::aligned;
     using gdn_host::fail;
     int st = check_common("prefill", H, dk, dv);
@@ -1460,6 +1469,7 @@ int prefill_batch(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
     p.out = out;
     p.state_out = state_out;
     p.cu = nullptr;
+    p.out_tm = out_tm;
     p.dt_bias = dt_bias;
     p.scale = scale == 0.f ? 1.f / sqrtf(static_cast<float>(dk)) : scale;
     p.H = H;
@@ -1494,6 +1504,14 @@ int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* 
                     int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
     return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
                          dv, workspace, workspace_bytes, stream, 3);
+}
+
+int gdn_prefill_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                       const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                       const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H,
+                       int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
+    return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
+                         dv, workspace, workspace_bytes, stream, 3, 1);
 }
 
 int gdn_prefill_intra_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,

@@ -9,8 +9,8 @@ Pipeline per call (all GPU, one stream):
 
   forward  RMSNorm kernel -> one fused q/k/v/a/b in-projection GEMM with the
            conv + SiLU epilogue writing the prefill kernel's head-major layout
-           (and, on request, the conv cache for decode) -> chunked prefill ->
-           W_o GEMM.  No .item() host sync: dt_bias is read once at
+           (and, on request, the conv cache for decode) -> chunked prefill
+           (output written token-major) -> W_o GEMM.  No .item() host sync: dt_bias is read once at
            construction (call ``refresh()`` after changing the weights).
   decode   RMSNorm kernel -> xn W^T GEMM -> decode conv step over the cached
            projections -> decode kernel (state update in place when asked)
@@ -142,9 +142,10 @@ class GDNLayerCustom:
         s_in = st.get('recurrent')
         if s_in is None:
             s_in = torch.empty(0, dtype=torch.float32, device=x.device)
+        # token-major output [B, T, H, dv]: feeds W_o without a transpose copy
         o, S = self.exts['prefill'].prefill(q, k, v, self.A_log, a, self.dt_bias_scalar, b, mask.contiguous(),
-                                            s_in, self.scale)
-        y = o.transpose(1, 2).reshape(B, T, Hh * dv) @ self.W_o.T
+                                            s_in, self.scale, token_major=True)
+        y = o.reshape(B, T, Hh * dv) @ self.W_o.T
         if not return_state:
             return y
         nc = self.CK - 1

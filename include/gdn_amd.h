@@ -91,6 +91,21 @@ int gdn_prefill_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* 
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * gdn_prefill_hip with the output written token-major: out [B, T, H, dv]
+ * (the layout the output projection consumes, so the caller's
+ * transpose(1, 2).contiguous() copy disappears); all else identical.
+ * Replaces the transposes around the prefill call in the reference layer
+ * (gdn_layer.py:256-263), which has no kernel-level counterpart.
+ */
+int gdn_prefill_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                       const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                       const gdn_bf16_t* b_logits, const float* mask,
+                       const float* state_in, float scale,
+                       gdn_bf16_t* out, float* state_out,
+                       int B, int H, int T, int dk, int dv,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * The two phases of gdn_prefill_hip, same arguments, for callers that overlap
  * them with other work (and for per-phase timing):
  *   intra — every chunk in parallel: reads q, k, a, b_logits, mask, A_log,

@@ -99,8 +99,10 @@ def test_binding_module_api_matches_reference():
     pf = exts["prefill"]
     assert (pf.H_DIM, pf.K_DIM, pf.V_DIM, pf.C_DIM) == (16, 128, 256, 64)
     sig = pf.prefill.__doc__.split("(", 1)[1].split(")", 1)[0]
-    assert [a.split(":")[0].strip() for a in sig.split(",")] == \
-        ["q", "k", "v", "A_log", "a", "dt_bias", "b_logits", "mask", "state_in", "scale"]
+    names = [a.split(":")[0].strip() for a in sig.split(",")]
+    # the reference's ten positional arguments, then keyword-only additions
+    assert names[:10] == ["q", "k", "v", "A_log", "a", "dt_bias", "b_logits", "mask", "state_in", "scale"]
+    assert names[10:] == ["*", "token_major"]
     for mod in ("decode", "rmsnorm", "proj"):
         assert hasattr(exts[mod], "forward")
 

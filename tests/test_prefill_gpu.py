@@ -146,6 +146,38 @@ def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
     assert_state_close(S, S_ref)
 
 
+@pytest.mark.parametrize("B,H,T,dv", [(1, 16, 8192, 128), (2, 3, 130, 128), (1, 2, 1500, 64), (3, 5, 100, 48),
+                                       (2, 4, 257, 256)])
+def test_prefill_token_major_output(exts, dev, B, H, T, dv):
+    """token_major=True (gdn_prefill_tm_hip) writes out [B, T, H, dv]: the same
+    numbers as the head-major [B, H, T, dv] call, bit for bit, transposed --
+    with chunk groups (the metric shape), ragged last chunks, 16/32-column tiles
+    and dv = 256; and the same through the C ABI."""
+    from gdn_18646_amd import abi
+    d = synth.prefill_inputs(B, T, H, 128, dv, seed=T + H, state=True)
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    args = (g["q"], g["k"], g["v"], g["A_log"], g["a"], float(g["dt_bias"]), g["b_logits"], g["mask"],
+            g["state_in"], 0.0)
+    out_hm, S_hm = exts["prefill"].prefill(*args)
+    out_tm, S_tm = exts["prefill"].prefill(*args, token_major=True)
+    torch.cuda.synchronize()
+    assert out_tm.shape == (B, T, H, dv) and out_tm.is_contiguous()
+    assert torch.equal(out_tm.cpu(), out_hm.transpose(1, 2).cpu())
+    assert torch.equal(S_tm.cpu(), S_hm.cpu())
+    # the C ABI entry point, on torch's current stream
+    out_c = torch.full_like(out_tm, float("nan"))
+    S_c = torch.empty_like(S_tm)
+    ws_bytes = abi.load().gdn_prefill_workspace_bytes(B, H, T, 128, dv)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    abi.call("gdn_prefill_tm_hip", g["q"].data_ptr(), g["k"].data_ptr(), g["v"].data_ptr(), g["A_log"].data_ptr(),
+             g["a"].data_ptr(), float(g["dt_bias"]), g["b_logits"].data_ptr(), g["mask"].data_ptr(),
+             g["state_in"].data_ptr(), 0.0, out_c.data_ptr(), S_c.data_ptr(), B, H, T, 128, dv, ws.data_ptr(),
+             ws_bytes, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out_c.cpu(), out_tm.cpu())
+    assert torch.equal(S_c.cpu(), S_tm.cpu())
+
+
 def test_prefill_varlen_chunk_groups(exts, dev):
     """Packed sequences of very different lengths with chunk groups: the short
     ones leave most of their groups empty (identity maps).  Slow decay, as above."""
