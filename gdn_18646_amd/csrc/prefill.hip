@@ -1297,6 +1297,13 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
         G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
     if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
     s.G = G < 2 ? 1 : static_cast<int>(G);
+    // A map pass that would fill at most half the CUs (few groups, e.g. G = 2
+    // at 128 (sequence, head) pairs) splits each group's dv + 128 columns over
+    // workgroups of 8 waves x 16 columns instead (psi and phi apart).
+    if (s.G > 1 && s.NT_map == 2 && s.NW_map == 8 && nheads * (s.G - 1) * s.nvg_map * 2 <= 256) {
+        s.NT_map = 1;
+        s.nvg_map = (dv + kDK) / 128;
+    }
     return s;
 }
 
@@ -1342,7 +1349,7 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
             }
             return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
         case 8:
-            if constexpr ((MODE == kModeMap && NT == 2) || (MODE == kModeOut && NT == 1)) {
+            if constexpr ((MODE == kModeMap && NT <= 2) || (MODE == kModeOut && NT == 1)) {
                 hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 8, NT>), grid, dim3(512), 0, stream, p, sg);
                 break;
             }

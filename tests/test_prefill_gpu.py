@@ -126,13 +126,14 @@ def test_prefill_state_composition_full_size(exts, dev):
 
 
 @pytest.mark.parametrize("B,H,T,dv,masked", [(1, 1, 4000, 16, False), (1, 2, 1500, 64, True),
-                                              (2, 1, 2600, 48, True)])
+                                              (2, 1, 2600, 48, True), (8, 16, 650, 128, True)])
 def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
     """Few (sequence, head) pairs and long sequences: the state pass splits each
     sequence into chunk groups and joins them through the groups' affine maps
-    (6 to 13 groups here, with 16- and 32-column tiles).  Slow decay (A_log = -8,
-    about 0.9998 per token) so the state carried into each group matters: a wrong
-    transition map would show at O(1)."""
+    (2 to 13 groups here, with 16- and 32-column tiles; at 128 pairs and two
+    groups the map pass runs psi and phi in separate 16-column workgroups).  Slow
+    decay (A_log = -8, about 0.9998 per token) so the state carried into each
+    group matters: a wrong transition map would show at O(1)."""
     d = synth.prefill_inputs(B, T, H, 128, dv, seed=T + dv, state=True)
     d["A_log"] = torch.linspace(-8.0, -2.0, H)
     mask = None
