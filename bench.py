@@ -241,13 +241,23 @@ def main():
         for _ in range(3):
             layer_dec()
         ms_ld = time_events(layer_dec, 128, torch)
+        step_g = layer.capture_decode(st_l)
+        it_g = iter(range(10 ** 9))
+
+        def layer_dec_graph():
+            step_g(xd[next(it_g) % len(xd)])
+
+        for _ in range(3):
+            layer_dec_graph()
+        ms_ldg = time_events(layer_dec_graph, 128, torch)
         layer_e2e = {"config": "hidden 2048, H=16, dk=dv=128, conv 4, weights N(0, 0.02); prefill B=4 x T=4096, "
                                "then decode steps at B=4 continuing from the prefill state",
                      "prefill_ms": ms_lf, "prefill_tokens_per_s": LB * LT / (ms_lf / 1e3),
-                     "decode_ms_per_step": ms_ld, "decode_steps_per_s": 1e3 / ms_ld}
+                     "decode_ms_per_step": ms_ld, "decode_steps_per_s": 1e3 / ms_ld,
+                     "decode_graph_ms_per_step": ms_ldg, "decode_graph_steps_per_s": 1e3 / ms_ldg}
         log(f"layer (config 5): prefill B={LB} T={LT} {ms_lf:.3f} ms ({LB * LT / (ms_lf / 1e3):.4g} tok/s), "
-            f"decode B={LB} {ms_ld * 1e3:.1f} us/step")
-        del layer, wl, xl, st_l
+            f"decode B={LB} {ms_ld * 1e3:.1f} us/step eager, {ms_ldg * 1e3:.1f} us/step as a HIP graph")
+        del layer, wl, xl, st_l, step_g
 
     # ------------------------------------------------------------------ CPU oracle
     cpu_prefill = cpu_decode = None

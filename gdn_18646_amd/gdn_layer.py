@@ -180,9 +180,46 @@ class GDNLayerCustom:
         y = o.to(x.dtype).reshape(B, 1, Hh * dv) @ self.W_o.T
         xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
         if inplace:
-            state['xn'] = xn_hist.contiguous()
+            state['xn'].copy_(xn_hist)  # same tensor, so a captured step stays valid
             return y, state
         return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist.contiguous())
+
+    def capture_decode(self, state, warmup=2):
+        """One in-place decode step of this layer captured as a HIP graph.
+
+        Returns ``step(x) -> y``: copies x [B, 1, D] into the graph's input
+        buffer, replays the graph and returns its output buffer (y [B, 1, D],
+        overwritten by the next call).  ``state`` (a decode-state dict, e.g.
+        from ``forward(..., return_state=True)``) is updated in place by
+        every call, exactly as ``decode(x, state, inplace=True)``.  The decode
+        step is a chain of small launches, so replaying it as one graph
+        removes the per-launch host overhead.  The warm-up steps run on copies
+        of the state values, which are then restored.
+        """
+        B = state['recurrent'].shape[0]
+        dev = state['recurrent'].device
+        x_static = torch.zeros(B, 1, self.D, dtype=torch.bfloat16, device=dev)
+        saved = {k: v.clone() for k, v in state.items()}
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self.decode(x_static, state, inplace=True)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        for k, v in state.items():
+            v.copy_(saved[k])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y_static, _ = self.decode(x_static, state, inplace=True)
+        del saved
+
+        def step(x):
+            x_static.copy_(x)
+            graph.replay()
+            return y_static
+
+        step.graph = graph
+        return step
 
 
 def _layer_module(exts):

@@ -88,6 +88,32 @@ def test_prefill_hands_off_to_decode(dev):
     assert_out_close(torch.cat([y_a, y_b], 1), y_full, what="prefill + prefill vs prefill")
 
 
+def test_layer_decode_graph_replays_match_eager(dev):
+    """capture_decode: one decode step as a HIP graph.  Every replay (with eager
+    work and a synchronisation between replays) must give the eager step's
+    output and state: the captured chain holds no memset nodes and reads the
+    state dict's tensors in place."""
+    w_cpu, w = _weights(dev, seed=3)
+    layer = GDNLayerCustom(w)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(3, 70, 256, generator=g).bfloat16().to(dev)
+    _, st = layer.forward(x, return_state=True)
+    st_eager = {k: v.clone() for k, v in st.items()}
+    st_graph = {k: v.clone() for k, v in st.items()}
+    step = layer.capture_decode(st_graph)
+    for k in st:  # capture leaves the state as it was
+        assert torch.equal(st_graph[k], st_eager[k]), k
+    for i in range(6):
+        xt = torch.randn(3, 1, 256, generator=g).bfloat16().to(dev)
+        y_e, st_eager = layer.decode(xt, st_eager, inplace=True)
+        y_g = step(xt).clone()
+        torch.cuda.synchronize()
+        _ = (xt.float() * 2).sum().item()  # unrelated eager work between replays
+        assert_out_close(y_g.cpu(), y_e.cpu(), atol=1e-3, rtol=1e-3, what=f"replay {i} output")
+        for k in st:
+            assert torch.allclose(st_graph[k].float(), st_eager[k].float(), atol=1e-6, rtol=1e-5), (i, k)
+
+
 def test_layer_config5_shapes(dev):
     """Brief config 5 dims (hidden 2048, H=16, d=128, conv 4, std 0.02): a short
     slice against the baseline, then the full B=4 x T=4096 prefill and 128 decode steps."""
