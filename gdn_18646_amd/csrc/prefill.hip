@@ -539,47 +539,6 @@ struct Stage {
 };
 
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) unsigned char lds_u8;
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
-typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
-typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
-typedef __attribute__((address_space(3))) float lds_f32;
-typedef __attribute__((address_space(3))) uint16_t lds_u16;
-
-// 16 bytes per lane from sbase + voff (sbase uniform over the wave, voff the
-// lane's 32-bit byte offset) to lds_base + 16 lane (lds_base uniform).
-// Asynchronous: completion is vmcnt.  The scalar-base form keeps source
-// addresses to one 32-bit register per lane: 64-bit per-lane pointers spill
-// in the state kernels, and a spill reload between copies makes the compiler
-// wait for every copy issued before it.  Issued as inline asm so the
-// compiler's wait-count pass does not drain the copy before unrelated LDS
-// reads of the other buffer (it cannot prove they do not alias); the kernels
-// order copies with their own vmcnt waits and barriers.  M0 is otherwise
-// unused on gfx950 (LDS instructions do not read it), so the clobber is safe.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, lds_u8* lds_base) {
-    const uint32_t m0v = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0v), "v"(voff), "s"(sbase)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// Workgroup barrier for LDS producer/consumer hand-off: LDS writes of this
-// wave complete, then all waves meet.  (Async copies are covered by the
-// vmcnt wait that precedes it.)
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// vmcnt(N) with the other counters open (gfx9 layout: vmcnt[3:0] | expcnt[6:4]
-// | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).  Vector memory ops retire in issue
-// order, so vmcnt(N) means "all but the last N issued have completed".
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
 
 // Per-lane byte offsets of the staging copies, fixed for the whole kernel.
 struct StageLane {

@@ -5,16 +5,31 @@
 // for the math.  P = x W^T is accumulated in fp32 and never rounded before the
 // conv (as the reference kernel does; the PyTorch reference rounds P to bf16).
 //
-// Tiling: a workgroup computes a 128 x 128 tile of P whose 128 GEMM rows are
-// the tokens t0-3 .. t0+124 of one sequence; the first 3 rows are the causal
-// halo, recomputed instead of exchanged, and 125 outputs are produced.
-// 4 waves in a 2 x 2 grid, each 64 x 64 = 4 x 4 MFMA 16x16x32 tiles; K steps
-// of 64 staged through LDS with the next step prefetched into registers.
-// The epilogue parks P in LDS (fp32) and applies conv + SiLU per column.
+// Two kernels:
+//
+// gdn_proj_conv_mfma_kernel (the fast path) computes the transposed product
+// P^T = W x^T in 256-column x 256-token tiles, one workgroup of 8 waves per
+// CU.  Rows run over a flattened token axis where each sequence is 3 cache
+// rows followed by its T tokens; a tile's first 3 rows are the causal halo
+// (recomputed), so 253 rows are written per tile, and cache rows take the
+// conv cache (or zero) so no tap reaches into another sequence.  Operands
+// reach LDS by DMA (global_load_lds) in two 64-wide K stages: every 8 lanes
+// of a copy read one whole 128-byte line (a row's K slice), placed with an
+// XOR swizzle that keeps the MFMA fragment reads at linear-read speed.
+// Waves form a 4 x 2 grid of 64 columns x 128 tokens = 4 x 8 MFMA 16x16x32
+// tiles.  In the transposed C layout a lane holds 4 adjacent columns of one
+// token and the 16 tokens of a tile form one DPP row: the conv taps are row
+// shifts, and stores are 8 bytes.
+//
+// gdn_proj_conv_kernel (general shapes: group boundaries not on 4 columns,
+// unaligned outputs, K not a multiple of 64) computes 128 x 128 tiles of P whose rows are
+// tokens t0-3 .. t0+124 of one sequence and parks P in LDS for the conv.
 //
 // Output routing: up to 5 column groups, each written either token-major
 // [B, T, width] or head-major [B, width/hd, T, hd], with or without the
 // conv + SiLU (a plain projection takes the current token's row of P).
+#include <type_traits>
+
 #include "gdn_common.hpp"
 #include "proj.hpp"
 
@@ -170,12 +185,405 @@ __global__ __launch_bounds__(256, 2) void gdn_proj_conv_kernel(gdn_proj::ProjPar
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Fast path: transposed MFMA tiles, DMA staging, register epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kMCols = 256;                   // output columns (W rows) per workgroup
+constexpr int kMToks = 256;                   // token rows per workgroup
+constexpr int kMOut = kMToks - kHalo;         // 253 tokens written per workgroup
+constexpr int kMK = 64;                       // K per stage: one 128-byte line per row
+constexpr int kMStages = 2;
+constexpr int kWMT = 4;                       // 16-column MFMA tiles per wave
+constexpr int kWNT = 8;                       // 16-token MFMA tiles per wave (128 tokens: 2 token waves)
+constexpr int kMWaves = (kMCols / (16 * kWMT)) * (kMToks / (16 * kWNT));
+constexpr int kMRowB = kMK * 2;               // 128 bytes per staged row
+constexpr int kMStageB = (kMCols + kMToks) * kMRowB;  // 64 KiB: W rows, then x rows
+constexpr int kMDma = (kMCols + kMToks) / 8 / kMWaves;  // 1 KiB copies (8 rows) per wave per stage
+static_assert((kMCols + kMToks) % (8 * kMWaves) == 0 && kMCols % (8 * kMWaves) == 0, "copies split evenly");
+static_assert(kMToks == 2 * 16 * kWNT, "two token waves");
+
+// Staged row r holds its 8 16-byte chunks (k 8c .. 8c+7) at slot c ^ (r & 7):
+// a fragment read (16 rows, one chunk each) then spreads every 8 consecutive
+// rows over the 8 slots of a 128-byte line, which reads at the rate of a
+// linear ds_read_b128 on gfx950 (measured; (r ^ (r >> 3)) & 7 lost a third).
+__device__ __forceinline__ int swz(int r) { return r & 7; }
+
+// Token n - K of a 16-token tile held one token per lane of a DPP row:
+// row_shr:K inside the tile; lanes n < K take token 16 + n - K of the
+// previous tile (row_ror:K of prev).
+template <int K>
+__device__ __forceinline__ float tap_prev(float cur, float prev) {
+    const int rot = __builtin_amdgcn_mov_dpp(__float_as_int(prev), 0x120 + K, 0xf, 0xf, true);  // every lane valid
+    return __int_as_float(__builtin_amdgcn_update_dpp(rot, __float_as_int(cur), 0x110 + K, 0xf, 0xf, false));
+}
+
+// x * sigmoid(x) with the hardware exp2 and reciprocal (about 1 ulp each).
+__device__ __forceinline__ float silu_f(float x) {
+    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// Two floats -> two round-to-nearest-even bf16 in one word (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+// Compile-time loop: f(integral_constant<int, I>) for I in [B, E).  Keeps
+// register-array indices constant from the first optimisation pass on.
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& fn) {
+    if constexpr (B < E) {
+        fn(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(fn);
+    }
+}
+
+// The group holding column c, by compare-and-select over constant indices
+// (indexing the parameter block with a runtime index would copy it to
+// private memory).
+__device__ __forceinline__ gdn_proj::ProjGroup select_group(const gdn_proj::ProjParams& p, int c) {
+    gdn_proj::ProjGroup g = p.groups[0];
+#pragma unroll
+    for (int q = 1; q < gdn_proj::kMaxGroups; ++q)
+        if (q < p.ngroups && c >= p.groups[q].col0) g = p.groups[q];
+    return g;
+}
+
+__global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kMWaves / 4, kMWaves / 4))) void gdn_proj_conv_mfma_kernel(
+    gdn_proj::ProjParams p, int n_tok, int n_col) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[kMStages * kMStageB];
+    lds_u8* const smem = (lds_u8*)&smem_raw[0];
+
+    // Workgroup -> tile.  Dispatch deals workgroups to the 8 XCDs round-robin;
+    // give each XCD a contiguous range of tiles, ordered in bands of 4 column
+    // tiles with the token tile slowest, so the workgroups resident on one
+    // XCD share W and x tiles in its L2.
+    const int ntiles = n_tok * n_col;
+    int lin;
+    {
+        const int id = blockIdx.x, xcd = id & 7, j = id >> 3, q = ntiles >> 3, r = ntiles & 7;
+        lin = xcd < r ? xcd * (q + 1) + j : r * (q + 1) + (xcd - r) * q + j;
+        const int band = lin / (4 * n_tok), base = 4 * band, gs = min(n_col - base, 4);
+        const int within = lin - band * 4 * n_tok;
+        lin = (within / gs) * n_col + base + within % gs;
+    }
+    const int tile_t = lin / n_col, tile_c = lin % n_col;
+    // Row space: each sequence is kHalo cache rows (t = -3 .. -1) followed by
+    // its T tokens, so row r is (b, t) = (r / T3, r % T3 - 3).  Cache rows
+    // take the cached projections (or zero) after the product, so conv taps
+    // never reach into another sequence.
+    const int T3 = p.T + kHalo;
+    const int F3 = p.B * T3;
+    const int f0 = tile_t * kMOut - kHalo;  // row of tile row 0 (>= -3; rows < 0 are never used)
+    const int c0 = tile_c * kMCols;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: DMA bases stay scalar
+    const int wm = wave >> 1, wn = wave & 1;                      // column slice, 128-token half
+    const int r16 = lane & 15, g4 = lane >> 4;
+
+    // x row feeding row r: the token itself, the sequence's first token for
+    // cache rows, clamped at both ends (those products are never used).
+    auto xrow_of = [&](int r) {
+        if (r < 0) return 0;
+        if (r >= F3) return p.B * p.T - 1;
+        const int b = r / T3, t = r - b * T3 - kHalo;
+        return b * p.T + max(t, 0);
+    };
+
+    // DMA sources.  Copy j of a wave moves staged rows 8 q .. 8 q + 7 with
+    // q = wave + 8 j (q < 32: W rows, else x rows); lane l takes row 8 q + l / 8
+    // and fills slot l % 8 with chunk (l % 8) ^ swz(row): every 8 lanes read
+    // one whole 128-byte line.  Columns >= D_out are clamped to a valid row;
+    // their products are never stored.
+    const int xrow0 = xrow_of(f0);
+    const unsigned char* wsrc = reinterpret_cast<const unsigned char*>(p.W + static_cast<size_t>(c0) * p.D);
+    const unsigned char* xsrc = reinterpret_cast<const unsigned char*>(p.x + static_cast<size_t>(xrow0) * p.D);
+    uint32_t voff[kMDma];
+#pragma unroll
+    for (int j = 0; j < kMDma; ++j) {
+        const int q = wave + kMWaves * j;
+        const int srow = 8 * q + (lane >> 3);  // staged row
+        int row;
+        if (srow < kMCols) {
+            row = min(c0 + srow, p.D_out - 1) - c0;
+        } else {
+            row = xrow_of(f0 + srow - kMCols) - xrow0;
+        }
+        const int chunk = (lane & 7) ^ swz(srow);
+        voff[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.D) * 2u + 16u * chunk;
+    }
+    auto issue_copy = [&](int stage, int kk, int j) {
+        const int q = wave + kMWaves * j;
+        const unsigned char* src = (8 * q < kMCols ? wsrc : xsrc) + kk * kMRowB;
+        dma16(src, voff[j], smem + stage * kMStageB + q * 1024);
+    };
+    auto issue = [&](int stage, int kk) {
+#pragma unroll
+        for (int j = 0; j < kMDma; ++j) issue_copy(stage, kk, j);
+    };
+    // Half `half` of a stage's copies.
+    auto issue_part = [&](int stage, int kk, int half) {
+#pragma unroll
+        for (int j = 0; j < kMDma / 2; ++j) issue_copy(stage, kk, half * kMDma / 2 + j);
+    };
+
+    // Fragment reads: lane l takes row 16 f + l % 16, chunk 4 h + l / 16 of
+    // the staged rows (h: which 32-wide half of the stage's K); rd[h] is the
+    // lane's byte offset within the fragment.
+    uint32_t rd[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) rd[h] = r16 * kMRowB + 16u * ((4 * h + g4) ^ swz(r16));
+
+    // Conv weights of this lane's columns, fetched now so their latency hides
+    // under the main loop: for conv_k == 4 the 4 columns' taps are 16
+    // adjacent bf16 (32-byte aligned: groups start on 4 columns).
+    u32x4 wraw[kWMT][2];
+#pragma unroll
+    for (int mt = 0; mt < kWMT; ++mt) {
+        wraw[mt][0] = wraw[mt][1] = u32x4{0u, 0u, 0u, 0u};
+        const int cb = c0 + 16 * kWMT * wm + 16 * mt + 4 * g4;
+        if (cb < p.D_out && p.conv_k == 4) {
+            const gdn_proj::ProjGroup gq = select_group(p, cb);
+            if (gq.conv) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(p.conv_w + static_cast<size_t>(gq.cw_row0 + cb - gq.col0) * 4);
+                wraw[mt][0] = src[0];
+                wraw[mt][1] = src[1];
+            }
+        }
+    }
+
+    f32x4 acc[kWMT][kWNT];
+#pragma unroll
+    for (int mt = 0; mt < kWMT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kWNT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = p.D / kMK;
+    issue(0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_vm<0>();
+        lds_barrier();  // stage kt landed for every wave; the other stage fully read
+        // The next stage's copies go out in two halves, one before each K
+        // half's MFMAs: a wave that issues all of them at once stalls on
+        // the copy queue before its first MFMA.
+        const bool next = kt + 1 < nk;
+        const lds_u8* st = smem + (kt & 1) * kMStageB;
+        static_for<0, 2>([&](auto H) {
+            constexpr int h = decltype(H)::value;
+            if (next) issue_part((kt + 1) & 1, kt + 1, h);
+            bf16x8 a[kWMT], bx[kWNT];
+            static_for<0, kWMT>([&](auto MT) {
+                constexpr int mt = decltype(MT)::value;
+                a[mt] = *reinterpret_cast<const lds_bf16x8*>(st + (16 * kWMT * wm + 16 * mt) * kMRowB + rd[h]);
+            });
+            static_for<0, kWNT>([&](auto NT) {
+                constexpr int nt = decltype(NT)::value;
+                bx[nt] = *reinterpret_cast<const lds_bf16x8*>(st + (kMCols + 16 * kWNT * wn + 16 * nt) * kMRowB + rd[h]);
+            });
+#pragma unroll
+            for (int nt = 0; nt < kWNT; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < kWMT; ++mt) acc[mt][nt] = mfma16x16x32(a[mt], bx[nt], acc[mt][nt]);
+        });
+    }
+
+    // The token waves meet at token 128: the wn = 1 wave's first tile takes
+    // its conv taps from the wn = 0 wave's last tile, handed over through the
+    // stage the last K step did not read (no copy targets it any more).
+    const lds_u8* xs = smem + (nk & 1) * kMStageB + wm * kWMT * 1024 + lane * 16;
+    if (wn == 0) {
+#pragma unroll
+        for (int mt = 0; mt < kWMT; ++mt)
+            *reinterpret_cast<lds_f32x4*>(const_cast<lds_u8*>(xs) + mt * 1024) = acc[mt][kWNT - 1];
+    }
+    lds_barrier();
+
+    // This lane's row in token tile 0 of the wave, as (b, t3 = t + 3); tile
+    // nt adds 16 rows.  Rows before local row kHalo are the tile's halo.
+    const int nloc0 = 16 * kWNT * wn + r16;
+    auto split = [&](int r, int& b, int& t3) {
+        b = r < 0 ? 0 : r / T3;
+        t3 = r - b * T3;
+    };
+    int b0, t30;
+    split(f0 + nloc0, b0, t30);
+    int bx, t3x;  // row of the handed-over tile (16 rows before tile 0)
+    split(f0 + nloc0 - 16, bx, t3x);
+    const int ncache = p.conv_k - 1;
+    // Lean epilogue when the wave's 16 kWNT rows are all tokens of one
+    // sequence (no cache rows, no sequence start) and none of them is in the
+    // conv cache refresh window (the last ncache tokens).
+    bool lean;
+    {
+        const int R0 = f0 + 16 * kWNT * wn;
+        int bR, t3R;
+        split(R0, bR, t3R);
+        lean = R0 >= 0 && R0 + 16 * kWNT <= F3 && t3R >= kHalo && t3R + 16 * kWNT <= T3 - ncache;
+    }
+
+    static_for<0, kWMT>([&](auto MT) {
+        constexpr int mt = decltype(MT)::value;
+        const int cb = c0 + 16 * kWMT * wm + 16 * mt + 4 * g4;  // this lane's 4 columns (same for the whole DPP row)
+        if (cb >= p.D_out) return;
+        const gdn_proj::ProjGroup gq = select_group(p, cb);
+        const int cc = cb - gq.col0, width = gq.width, hd = gq.head_dim;
+        const bool conv = gq.conv != 0;
+        // Element index of (b, t, column cc + i): b width T + t tstride + coff[i]
+        // (token-major: tstride = width, coff = cc + i; head-major [B, width/hd,
+        // T, hd]: tstride = hd, coff = ((cc + i) / hd) T hd + (cc + i) % hd).
+        const size_t seq = static_cast<size_t>(width) * p.T;
+        const int tstride = hd ? hd : width;
+        const bool vec = hd == 0 || (hd & 3) == 0;  // the 4 columns are adjacent in memory
+        size_t coff[4];
+        {
+            int h = hd ? cc / hd : 0, d = hd ? cc - h * hd : cc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                coff[i] = hd ? static_cast<size_t>(h) * p.T * hd + d : static_cast<size_t>(cc + i);
+                if (hd && ++d == hd) {
+                    d = 0;
+                    ++h;
+                }
+            }
+        }
+        float w[4][4];  // [column][tap], taps right-aligned: tap 3 multiplies the current token
+        if (p.conv_k == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 q = wraw[mt][i >> 1];
+                const uint32_t lo = q[2 * (i & 1)], hi = q[2 * (i & 1) + 1];
+                w[i][0] = __uint_as_float(lo << 16);
+                w[i][1] = __uint_as_float(lo & 0xffff0000u);
+                w[i][2] = __uint_as_float(hi << 16);
+                w[i][3] = __uint_as_float(hi & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int jw = j - (4 - p.conv_k);  // weight index of tap j
+                    w[i][j] = conv && jw >= 0
+                                  ? bf2f(p.conv_w[static_cast<size_t>(gq.cw_row0 + cc + i) * p.conv_k + jw])
+                                  : 0.f;
+                }
+        }
+        // Cache row (t < 0) of a conv group: the cached projection of token t
+        // (cache index t + ncache, oldest first), zero before the cache or
+        // without one.
+        auto cache_row = [&](f32x4 v, int b, int t3) {
+            const int q = t3 - kHalo + ncache;
+            if (conv && t3 < kHalo) {
+                const uint16_t* cin = gq.cache_in;
+                const bool has = cin != nullptr && q >= 0;
+                const uint16_t* src = has ? cin + (static_cast<size_t>(b) * width + cc) * ncache + q : nullptr;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = has ? bf2f(src[i * ncache]) : 0.f;
+            }
+            return v;
+        };
+        f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (wn == 1) pv = cache_row(*reinterpret_cast<const lds_f32x4*>(xs + mt * 1024), bx, t3x);
+        // conv + SiLU of one 16-token tile (plain groups: the current row).
+        auto finish = [&](const f32x4 cur, float (&y)[4]) {
+            if (conv) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float s = w[i][3] * cur[i] + w[i][2] * tap_prev<1>(cur[i], pv[i]) +
+                                    w[i][1] * tap_prev<2>(cur[i], pv[i]) + w[i][0] * tap_prev<3>(cur[i], pv[i]);
+                    y[i] = silu_f(s);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[i] = cur[i];
+            }
+        };
+        auto store = [&](uint16_t* row, const float (&y)[4]) {
+            if (vec) {
+                *reinterpret_cast<u32x2*>(row + coff[0]) = u32x2{pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3])};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) row[coff[i]] = f2bf_bits(y[i]);
+            }
+        };
+        if (lean) {
+            // The wave's rows are tokens of one sequence, clear of its cache
+            // rows and of the cache refresh window: no per-row checks.
+            uint16_t* const row0 = gq.dst + static_cast<size_t>(b0) * seq + static_cast<size_t>(t30 - kHalo) * tstride;
+            static_for<0, kWNT>([&](auto NT) {
+                constexpr int nt = decltype(NT)::value;
+                const f32x4 cur = acc[mt][nt];
+                float y[4];
+                finish(cur, y);
+                pv = cur;
+                if (nt == 0 && nloc0 < kHalo) return;  // the tile's halo rows
+                store(row0 + static_cast<size_t>(16 * nt) * tstride, y);
+            });
+            return;
+        }
+        int b = b0, t3 = t30;
+        static_for<0, kWNT>([&](auto NT) {
+            constexpr int nt = decltype(NT)::value;
+            if (nt > 0) {
+                t3 += 16;
+                if (t3 >= T3) {
+                    b += t3 / T3;
+                    t3 %= T3;
+                }
+            }
+            const int nloc = nloc0 + 16 * nt;
+            const bool row_ok = nloc >= kHalo && f0 + nloc < F3;  // a row this tile owns
+            const int t = t3 - kHalo;
+            const f32x4 cur = cache_row(acc[mt][nt], b, t3);
+            float y[4];
+            finish(cur, y);
+            pv = cur;
+            if (!row_ok) return;
+            if (t >= 0) store(gq.dst + static_cast<size_t>(b) * seq + static_cast<size_t>(t) * tstride, y);
+            // New cache: rows t = T - ncache .. T - 1 of the extended sequence
+            // (cache rows included when T < ncache).
+            if (conv && gq.cache_out && t >= p.T - ncache) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    gq.cache_out[(static_cast<size_t>(b) * width + cc + i) * ncache + (t - (p.T - ncache))] =
+                        f2bf_bits(cur[i]);
+            }
+        });
+    });
+}
+
 }  // namespace
 
 namespace gdn_proj {
 
+// The fast kernel needs every group to start on a 4-column boundary (a lane's
+// 4 columns share a group), 8-byte aligned outputs for its vector stores,
+// 16-byte aligned conv weights (read 4 columns x 4 taps at a time) and 32-bit
+// DMA offsets.
+static bool mfma_path_ok(const ProjParams& p) {
+    if (p.D % kMK != 0 || p.D_out % 4 != 0) return false;
+    if (!gdn_host::aligned(p.conv_w, 16)) return false;
+    if (static_cast<long long>(p.D_out) * p.D * 2 >= (1ll << 31)) return false;
+    if (static_cast<long long>(kMToks) * p.D * 2 >= (1ll << 31)) return false;
+    if (static_cast<long long>(p.B) * (p.T + kHalo) >= (1ll << 30)) return false;
+    for (int g = 0; g < p.ngroups; ++g) {
+        const ProjGroup& q = p.groups[g];
+        if (q.col0 % 4 != 0 || q.width % 4 != 0 || q.cw_row0 % 4 != 0) return false;
+        if (!gdn_host::aligned(q.dst, 8)) return false;
+    }
+    return true;
+}
+
 int launch_proj(const ProjParams& p, hipStream_t stream) {
     if (p.B == 0 || p.T == 0 || p.D_out == 0) return GDN_OK;
+    if (mfma_path_ok(p)) {
+        const int F3 = p.B * (p.T + kHalo);  // rows: kHalo cache rows + T tokens per sequence
+        const int n_tok = (F3 + kMOut - 1) / kMOut, n_col = (p.D_out + kMCols - 1) / kMCols;
+        hipLaunchKernelGGL(gdn_proj_conv_mfma_kernel, dim3(n_tok * n_col), dim3(kMWaves * 64), 0, stream, p, n_tok, n_col);
+        return gdn_host::check_launch("gdn_proj_conv_mfma_kernel");
+    }
     const dim3 grid((p.T + kOutT - 1) / kOutT, (p.D_out + kBN - 1) / kBN, p.B);
     hipLaunchKernelGGL(gdn_proj_conv_kernel, grid, dim3(256), 0, stream, p);
     return gdn_host::check_launch("gdn_proj_conv_kernel");

@@ -86,3 +86,60 @@ def test_proj_conv_taps_and_ragged_Dout(exts, dev, ck, Dout):
     x, W, cw = _proj_case(3, 140, 192, Dout, ck=ck, seed=ck + Dout)
     y = exts["proj"].forward(x.to(dev), W.to(dev), cw.to(dev)).cpu()
     assert_out_close(y, ref_proj_conv_silu_f32(x, W, cw))
+
+
+@pytest.mark.parametrize("B,T", [(1, 253), (1, 254), (2, 253), (1, 509), (3, 300), (5, 131), (64, 1), (40, 2),
+                                 (30, 3), (9, 57)])
+def test_proj_flattened_token_tiles(exts, dev, B, T):
+    """The MFMA kernel tiles the flattened B*T token axis in 256-row tiles with 253
+    outputs: tile edges at multiples of 253, sequence starts inside a tile (their
+    taps must not reach into the previous sequence) and the hand-over between the
+    two 128-token waves of a tile (local tokens 128..130)."""
+    x, W, cw = _proj_case(B, T, 128, 160, seed=B * 7 + T)
+    y = exts["proj"].forward(x.to(dev), W.to(dev), cw.to(dev)).cpu()
+    assert_out_close(y, ref_proj_conv_silu_f32(x, W, cw))
+
+
+def _in_proj_expected(x, W, cw, H, dk, dv, caches):
+    """fp32 composition of the fused in-projection with conv caches: the conv runs
+    over cache ++ P (cache = projections of the 3 tokens before t = 0)."""
+    from oracle.proj_ref import ref_conv1d
+    B, T, _ = x.shape
+    nc = cw.shape[1] - 1
+    Hk, Hv = H * dk, H * dv
+    P = x.float() @ W.float().T
+    C = 2 * Hk + Hv
+    prefix = torch.cat(caches, 1).float().transpose(1, 2) if caches is not None else torch.zeros(B, nc, C)
+    ext = torch.cat([prefix, P[..., :C]], 1)
+    y = torch.nn.functional.silu(ref_conv1d(ext, cw.float())[:, nc:]).bfloat16()
+    hm = lambda t, d: t.reshape(B, T, H, d).transpose(1, 2)
+    outs = [hm(y[..., :Hk], dk), hm(y[..., Hk:2 * Hk], dk), hm(y[..., 2 * Hk:C], dv),
+            P[..., C:C + H].bfloat16().transpose(1, 2), P[..., C + H:].bfloat16().transpose(1, 2)]
+    tail = ext[:, -nc:].bfloat16().transpose(1, 2)  # [B, C, nc]
+    return outs, [tail[:, :Hk], tail[:, Hk:2 * Hk], tail[:, 2 * Hk:]]
+
+
+# H = 2 leaves the b group at column 2 H dk + H dv + H = 162 (not on a 4-column
+# boundary): the tiled kernel runs; H = 4 puts every group on one: the MFMA kernel.
+@pytest.mark.parametrize("H", [2, 4])
+@pytest.mark.parametrize("B,T", [(3, 1), (2, 3), (2, 5), (5, 70), (2, 300)])
+@pytest.mark.parametrize("with_cache", [False, True])
+def test_in_proj_matches_fp32_composition(dev, H, B, T, with_cache):
+    from gdn_18646_amd import native_extension
+    lay = native_extension().layer
+    dk, dv, D, ck = 32, 16, 128, 4
+    g = torch.Generator().manual_seed(H * 100 + B * 10 + T + int(with_cache))
+    Dout = 2 * H * dk + H * dv + 2 * H
+    x = torch.randn(B, T, D, generator=g).bfloat16()
+    W = (torch.randn(Dout, D, generator=g) * D ** -0.5).bfloat16()
+    cw = (torch.randn(Dout - 2 * H, ck, generator=g) * 0.5).bfloat16()
+    caches = None
+    if with_cache:
+        caches = [torch.randn(B, H * d, ck - 1, generator=g).bfloat16() for d in (dk, dk, dv)]
+    want = _in_proj_expected(x, W, cw, H, dk, dv, caches)
+    cd = [c.to(dev) for c in caches] if caches is not None else [None] * 3
+    got = lay.in_proj(x.to(dev), W.to(dev), cw.to(dev), H, dk, dv, *cd, True)
+    for name, y, r in zip("qkvab", got[:5], want[0]):
+        assert_out_close(y.cpu(), r, what=name)
+    for name, y, r in zip(("cache_q", "cache_k", "cache_v"), got[5:], want[1]):
+        assert_out_close(y.cpu(), r, atol=1e-2, rtol=1e-2, what=name)
