@@ -76,17 +76,26 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8 a, const bf16x8 b, co
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 pack8(const f32x4 lo, const f32x4 hi) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        r[i] = f2bf(lo[i]);
-        r[4 + i] = f2bf(hi[i]);
-    }
-    return r;
+// Two floats -> two round-to-nearest-even bf16 in one word: one
+// v_cvt_pk_bf16_f32 (converting element by element costs a convert per value
+// plus the shifts and ors that merge the halves).
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+// Four floats -> four bf16, as 8 bytes.
+__device__ __forceinline__ u32x2 pack4_bf16(const f32x4 v) {
+    return u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
+
+__device__ __forceinline__ bf16x8 pack8(const f32x4 lo, const f32x4 hi) {
+    return as_bf16x8(u32x4{pack2_bf16(lo[0], lo[1]), pack2_bf16(lo[2], lo[3]), pack2_bf16(hi[0], hi[1]),
+                           pack2_bf16(hi[2], hi[3])});
+}
 
 // ---------------------------------------------------------------------------
 // LDS staging by DMA (global_load_lds) and the waits that order it.

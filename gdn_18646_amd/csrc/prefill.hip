@@ -680,22 +680,15 @@ __device__ __forceinline__ bf16x8 ktfrag(const lds_u8* kbuf, uint32_t kt_lane, i
 // bf16 of (x - bf16(x)) for a pair of accumulator quads: the low half of a
 // two-term bf16 split.
 __device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const bf16x8 h) {
-    bf16x8 r;
+    f32x4 dl, dh;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        r[i] = f2bf(lo[i] - bf2f(h[i]));
-        r[4 + i] = f2bf(hi[i] - bf2f(h[4 + i]));
+        dl[i] = lo[i] - bf2f(h[i]);
+        dh[i] = hi[i] - bf2f(h[4 + i]);
     }
-    return r;
+    return pack8(dl, dh);
 }
 
-// Four floats -> four bf16 (round to nearest even), as 8 bytes.
-__device__ __forceinline__ u32x2 pack4_bf16(const f32x4 v) {
-    u32x2 r;
-    r[0] = static_cast<uint32_t>(f2bf_bits(v[0])) | (static_cast<uint32_t>(f2bf_bits(v[1])) << 16);
-    r[1] = static_cast<uint32_t>(f2bf_bits(v[2])) | (static_cast<uint32_t>(f2bf_bits(v[3])) << 16);
-    return r;
-}
 
 // One chunk of the state recurrence for a 128 x (16 NT) column tile, operands
 // in LDS.  `ob` points at out[row_base][0] (uniform).  Operand fragments are
@@ -1080,12 +1073,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 constexpr int kScanDepth = 6;
 constexpr int kMaxGroups = 16;  // chunk groups per sequence (plan_state caps G here)
 
-__device__ __forceinline__ u32x2 pack4_hi(const f32x4 v) {
-    u32x2 r;
-    r[0] = static_cast<uint32_t>(f2bf_bits(v[0])) | (static_cast<uint32_t>(f2bf_bits(v[1])) << 16);
-    r[1] = static_cast<uint32_t>(f2bf_bits(v[2])) | (static_cast<uint32_t>(f2bf_bits(v[3])) << 16);
-    return r;
-}
+__device__ __forceinline__ u32x2 pack4_hi(const f32x4 v) { return pack4_bf16(v); }
 // bf16 of (x - bf16(x)): the low part of a two-term bf16 split.
 __device__ __forceinline__ u32x2 pack4_lo(const f32x4 v, const u32x2 hi) {
     f32x4 d;

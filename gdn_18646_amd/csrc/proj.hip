@@ -223,13 +223,6 @@ __device__ __forceinline__ float silu_f(float x) {
     return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
-typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-// Two floats -> two round-to-nearest-even bf16 in one word (one v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
-}
-
 // Compile-time loop: f(integral_constant<int, I>) for I in [B, E).  Keeps
 // register-array indices constant from the first optimisation pass on.
 template <int B, int E, typename Fn>

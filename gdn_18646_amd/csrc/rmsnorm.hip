@@ -51,9 +51,7 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __rest
             u32x4 o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t lo = f2bf_bits((f[2 * e] * inv) * gm[2 * e]);
-                const uint32_t hi = f2bf_bits((f[2 * e + 1] * inv) * gm[2 * e + 1]);
-                o[e] = lo | (hi << 16);
+                o[e] = pack2_bf16((f[2 * e] * inv) * gm[2 * e], (f[2 * e + 1] * inv) * gm[2 * e + 1]);
             }
             yr[c] = o;
         }
