@@ -17,9 +17,11 @@ with the achieved MFMA / HBM roofline fractions.
 * ``cpu_baseline``: the CPU oracle (oracle/, a restatement of the reference's
   PyTorch code) timed on this host on the same inputs, and the same-run parity
   of the GPU results against it.
-* ``prefill_batches``: the same prefill at B=4 and B=8; ``layer_e2e``: the
-  end-to-end layer of config 5 (RMSNorm, fused projection + conv + SiLU,
-  prefill, output projection at B=4 x T=4096, then decode steps at B=4).
+* ``prefill_batches``: the same prefill at B=4 and B=8; ``prefill_varlen``:
+  config 3 (8 packed sequences, lengths U[512, 8192], nonzero initial
+  states); ``layer_e2e``: the end-to-end layer of config 5 (RMSNorm, fused
+  projection + conv + SiLU, prefill, output projection at B=4 x T=4096, then
+  decode steps at B=4).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-extra]
 """
@@ -100,7 +102,8 @@ def main():
     ap.add_argument("--B", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the B=4/8 prefill lines and the end-to-end layer (config 5) timing")
+                    help="skip the B=4/8 prefill lines, the packed varlen prefill (config 3) and the "
+                         "end-to-end layer (config 5) timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device copies of exactly 256 MiB (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -186,6 +189,28 @@ def main():
                                  "path_tflops": PREFILL_FLOP_PER_TOKEN_HEAD * Bx * T * H / (msx / 1e3) / 1e12}
             log(f"prefill B={Bx} T={T} H={H}: {msx:.4f} ms/step, {Bx * T / (msx / 1e3):.4g} tok/s")
             del dx, gx
+
+    # ------------------------------------- packed variable-length prefill (config 3)
+    varlen = None
+    if not args.no_extra:
+        lengths = synth.varlen_lengths(8, 512, 8192, seed=3)
+        dl = synth.varlen_inputs(lengths, H, K, V, seed=3)
+        gl_ = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in dl.items()}
+
+        def step_vl():
+            return pf.prefill_varlen(gl_["q"], gl_["k"], gl_["v"], gl_["A_log"], gl_["a"], 0.0, gl_["b_logits"],
+                                     gl_["cu_seqlens"], gl_["state_in"], 0.0)
+
+        for _ in range(2):
+            step_vl()
+        msv = time_events(step_vl, max(3, args.steps // 2), torch)
+        ntok = int(sum(lengths))
+        varlen = {"config": "8 packed sequences, lengths U[512, 8192] (seed 3): " + ",".join(map(str, lengths)) +
+                            f"; H={H}, dk=dv={K}, nonzero initial states",
+                  "tokens": ntok, "ms": msv, "tokens_per_s": ntok / (msv / 1e3),
+                  "path_tflops": PREFILL_FLOP_PER_TOKEN_HEAD * ntok * H / (msv / 1e3) / 1e12}
+        log(f"prefill varlen ({ntok} tokens in 8 sequences): {msv:.4f} ms/call, {ntok / (msv / 1e3):.4g} tok/s")
+        del dl, gl_
 
     # ------------------------------------------------------------------ decode
     DB, DH = 256, 32
@@ -349,6 +374,7 @@ def main():
             "path_flop": PREFILL_FLOP_PER_TOKEN_HEAD * tokens * H, "path_bytes": prefill_bytes(B, T, H),
         },
         "prefill_batches": batches or None,
+        "prefill_varlen": varlen,
         "layer_e2e": layer_e2e,
         "decode": {
             "value": 1e3 / ms_decode, "unit": "steps/s", "ms_per_step": ms_decode, "steps": args.decode_steps,
