@@ -197,9 +197,9 @@ def main():
         dl = synth.varlen_inputs(lengths, H, K, V, seed=3)
         gl_ = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in dl.items()}
 
-        def step_vl():
+        def step_vl():  # offsets from the host, as a serving loop has them
             return pf.prefill_varlen(gl_["q"], gl_["k"], gl_["v"], gl_["A_log"], gl_["a"], 0.0, gl_["b_logits"],
-                                     gl_["cu_seqlens"], gl_["state_in"], 0.0)
+                                     dl["cu_seqlens"], gl_["state_in"], 0.0)
 
         for _ in range(2):
             step_vl()

@@ -117,7 +117,7 @@ std::tuple<Tensor, Tensor> prefill_varlen(Tensor q, Tensor k, Tensor v, Tensor A
     TORCH_CHECK(A_log.numel() == H, "A_log must have H entries");
     TORCH_CHECK(cu_seqlens.dim() == 1 && cu_seqlens.numel() >= 2, "cu_seqlens must be [N + 1]");
     const int64_t N = cu_seqlens.numel() - 1;
-    // Validate offsets on the host (one small copy): kernels index with them.
+    // Validate offsets on the host: kernels index with them.
     auto cu_host = cu_seqlens.to(at::kCPU).to(at::kLong).contiguous();
     const int64_t* cu = cu_host.data_ptr<int64_t>();
     TORCH_CHECK(cu[0] == 0 && cu[N] == Ttot, "cu_seqlens must start at 0 and end at T_total");
@@ -143,7 +143,16 @@ std::tuple<Tensor, Tensor> prefill_varlen(Tensor q, Tensor k, Tensor v, Tensor A
         sin_ptr = state_in.data_ptr<float>();
     }
     const c10::DeviceGuard guard(q.device());
-    auto cu_dev = cu_host.to(at::kInt).to(q.device());
+    // Offsets given on the GPU are used in place (validating them above took
+    // one read back); offsets given on the host go up through pinned memory
+    // without blocking the host on the stream.
+    Tensor cu_dev;
+    if (cu_seqlens.is_cuda()) {
+        TORCH_CHECK(cu_seqlens.device() == q.device(), "cu_seqlens must be on q's device");
+        cu_dev = cu_seqlens.to(at::kInt).contiguous();
+    } else {
+        cu_dev = cu_host.to(at::kInt).pin_memory().to(q.device(), /*non_blocking=*/true);
+    }
     auto out = at::empty({1, H, Ttot, V}, q.options());
     auto state_out = at::empty({N, H, K, V}, q.options().dtype(at::kFloat));
     const size_t ws_bytes = gdn_prefill_varlen_workspace_bytes(N, H, Ttot, K, V);

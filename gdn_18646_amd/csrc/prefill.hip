@@ -891,7 +891,25 @@ struct StateGrid {
                      // state of group j + 1 in slot j
     uint16_t* phi;   // map pass: transitions as MFMA A fragments, [nheads][G][8][4][64][8]
                      // bf16 (row tile r, k-step, lane: row rho(r, n/4, n%4), columns 32ks + 8g..)
+    // Packed sequences: per-sequence group counts planned on the device
+    // (gdn_prefill_plan_kernel), or null for one group count G for all.
+    // Table: [0] slots (sum of G_i), [1] map slots (sum of G_i - 1), then
+    // (G_i, first slot of sequence i) for every sequence, then kPlanCap
+    // entries (sequence << 8 | group) for every slot, then kPlanCap for every
+    // map slot.  psi/phi of (sequence, head, group) sit at slot (first + group)
+    // x H + head instead of ((sequence H + head) G + group).
+    const int32_t* plan;
+    int nseq;
 };
+
+constexpr int kPlanCap = 256;  // slot table capacity (slots per head never exceed 256 / H)
+__device__ __forceinline__ int plan_groups(const StateGrid& sg, int sidx) { return sg.plan[2 + 2 * sidx]; }
+__device__ __forceinline__ int plan_first(const StateGrid& sg, int sidx) { return sg.plan[3 + 2 * sidx]; }
+// psi/phi unit of (sequence, head, group).
+__device__ __forceinline__ size_t group_unit(const StateGrid& sg, int H, int sidx, int h, int grp) {
+    return sg.plan ? static_cast<size_t>(plan_first(sg, sidx) + grp) * H + h
+                   : static_cast<size_t>(sidx * H + h) * sg.ngroups + grp;
+}
 
 // State pass over one chunk group per workgroup (NW waves, NT 16-column tiles
 // each, of one (sequence, head)).
@@ -913,18 +931,30 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 
     const int wg = blockIdx.x;
     const int nunits = sg.nheads * sg.ngroups_run;
-    int head, grp, vg;
-    if (p.xcd_heads) {
-        const HeadItem hi = head_major_xcd(wg, sg.ngroups_run * sg.nvg);
-        head = hi.head;
-        grp = hi.item / sg.nvg;
-        vg = hi.item % sg.nvg;
-    } else {
+    int head, grp, vg, ngroups;
+    if (sg.plan) {
+        // ngroups_run = slots per head in the grid: (head, slot, column part)
         vg = wg % sg.nvg;
-        head = (wg / sg.nvg) / sg.ngroups_run;
-        grp = (wg / sg.nvg) % sg.ngroups_run;
+        const int hh = (wg / sg.nvg) / sg.ngroups_run, q = (wg / sg.nvg) % sg.ngroups_run;
+        if (hh >= p.H || q >= sg.plan[MODE == kModeMap ? 1 : 0]) return;  // uniform over the workgroup
+        const int e = sg.plan[2 + 2 * sg.nseq + (MODE == kModeMap ? kPlanCap : 0) + q];
+        head = (e >> 8) * p.H + hh;
+        grp = e & 255;
+        ngroups = plan_groups(sg, e >> 8);
+    } else {
+        if (p.xcd_heads) {
+            const HeadItem hi = head_major_xcd(wg, sg.ngroups_run * sg.nvg);
+            head = hi.head;
+            grp = hi.item / sg.nvg;
+            vg = hi.item % sg.nvg;
+        } else {
+            vg = wg % sg.nvg;
+            head = (wg / sg.nvg) / sg.ngroups_run;
+            grp = (wg / sg.nvg) % sg.ngroups_run;
+        }
+        if (head * sg.ngroups_run + grp >= nunits) return;  // uniform over the workgroup
+        ngroups = sg.ngroups;
     }
-    if (head * sg.ngroups_run + grp >= nunits) return;  // uniform over the workgroup
     const int sidx = head / p.H;
     const int h = head % p.H;
     const SeqInfo sq = seq_info(p, sidx);
@@ -935,7 +965,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
     const int col0_wave = (vg * NW + wave) * 16 * NT;  // map pass: >= dv means identity columns
     const bool phi_cols = MODE == kModeMap && col0_wave >= dv;
     const int nchunks = (sq.len + kC - 1) / kC;
-    const int glen = (nchunks + sg.ngroups - 1) / sg.ngroups;
+    const int glen = (nchunks + ngroups - 1) / ngroups;
     const int c_begin = min(grp * glen, nchunks), c_end = min(c_begin + glen, nchunks);
     const StageLane L = {static_cast<uint32_t>(kslot_row(lane) * kDK * 2 + (lane >> 4) * 16),
                          static_cast<uint32_t>((lane & 15) * kDK * 2 + (lane >> 4) * 16),
@@ -960,7 +990,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const f32x4* Ps = reinterpret_cast<const f32x4*>(
-                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048);
+                sg.psi + (group_unit(sg, p.H, sidx, h, grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048);
 #pragma unroll
             for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r * 64 + lane];
         }
@@ -1019,7 +1049,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
     }
 
     if constexpr (MODE == kModeOut) {
-        if (grp != sg.ngroups - 1) return;
+        if (grp != ngroups - 1) return;
         float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
         for (int r = 0; r < 8; ++r)
@@ -1032,7 +1062,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
         // (a column per lane); a fragment lane needs 8 consecutive columns of
         // one row.  Transpose each 16x16 tile through this wave's own V area
         // (unused by identity columns), then store 512 contiguous bytes.
-        uint16_t* Ph = sg.phi + static_cast<size_t>(head * sg.ngroups + grp) * kDK * kDK;
+        uint16_t* Ph = sg.phi + group_unit(sg, p.H, sidx, h, grp) * kDK * kDK;
         lds_u16* tt = reinterpret_cast<lds_u16*>(buf0 + St::offV + wave * St::vWave);
 #pragma unroll
         for (int r = 0; r < 8; ++r)
@@ -1051,7 +1081,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             f32x4* Ps = reinterpret_cast<f32x4*>(
-                sg.psi + (static_cast<size_t>(head * sg.ngroups + grp) * (dv / 16) + col0_wave / 16 + nt) * 2048);
+                sg.psi + (group_unit(sg, p.H, sidx, h, grp) * (dv / 16) + col0_wave / 16 + nt) * 2048);
 #pragma unroll
             for (int r = 0; r < 8; ++r) Ps[r * 64 + lane] = S[r][nt];
         }
@@ -1087,7 +1117,9 @@ __device__ __forceinline__ u32x2 pack4_lo(const f32x4 v, const u32x2 hi) {
 // STEPS = G - 1 is a template parameter so that the step loop unrolls
 // completely with static register slots and exact wait counts (a rolled
 // loop makes the compiler wait for every outstanding load at its header).
-template <int STEPS>
+// PLANNED: per-sequence group counts (sg.plan); STEPS is then the most any
+// sequence can have and each workgroup stops after its own G_i - 1 steps.
+template <int STEPS, bool PLANNED>
 __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, StateGrid sg) {
     static_assert(STEPS >= 1 && STEPS < kMaxGroups, "scan steps");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * 8 * kFragB];
@@ -1104,6 +1136,8 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
         tile = blockIdx.x % ntile;
     }
     const int sidx = head / p.H, h = head % p.H;
+    const int nsteps = PLANNED ? plan_groups(sg, sidx) - 1 : STEPS;
+    if (PLANNED && nsteps <= 0) return;  // one group: nothing to compose
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = row tile r
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
@@ -1119,7 +1153,7 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
         S = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     auto psi_at = [&](int j) {
-        return reinterpret_cast<f32x4*>(sg.psi + (static_cast<size_t>(head * sg.ngroups + j) * ntile + tile) * 2048) +
+        return reinterpret_cast<f32x4*>(sg.psi + (group_unit(sg, p.H, sidx, h, j) * ntile + tile) * 2048) +
                wave * 64 + lane;
     };
     // This wave's phi fragments (row tile r, k-steps 0..3: 4 contiguous KiB)
@@ -1128,7 +1162,7 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
     u32x4 ph[D][4];
     f32x4 ps[D];
     auto load = [&](int j) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(sg.phi + static_cast<size_t>(head * sg.ngroups + j) * kDK * kDK) +
+        const u32x4* src = reinterpret_cast<const u32x4*>(sg.phi + group_unit(sg, p.H, sidx, h, j) * kDK * kDK) +
                            4 * wave * 64 + lane;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) ph[j % D][ks] = src[ks * 64];
@@ -1139,7 +1173,8 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
     };
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < D; ++j) load(j);
+    for (int j = 0; j < D; ++j)
+        if (!PLANNED || j < nsteps) load(j);
     const int half = (wave & 1) * 8;  // this row tile's bytes in its k-step's B fragment
     auto publish = [&](lds_u8* buf) {
         const u32x2 hi = pack4_hi(S);
@@ -1149,6 +1184,7 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
     publish(sbuf);
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
+        if (PLANNED && j >= nsteps) continue;  // uniform over the workgroup (the loop still unrolls)
         lds_u8* const buf = sbuf + (j & 1) * 8 * kFragB;
         lds_barrier();
         f32x4 acc_h = ps[j % D];
@@ -1159,7 +1195,7 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
             acc_h = mfma16x16x32(a, frag(buf, (2 * ks) * kFragB, lane), acc_h);
             acc_l = mfma16x16x32(a, frag(buf, (2 * ks + 1) * kFragB, lane), acc_l);
         }
-        if (j + D < STEPS) load(j + D);
+        if (j + D < STEPS && (!PLANNED || j + D < nsteps)) load(j + D);
         S = acc_h + acc_l;
         *psi_at(j) = S;
         publish(sbuf + ((j + 1) & 1) * 8 * kFragB);
@@ -1170,12 +1206,86 @@ template <int STEPS>
 int launch_scan(const PrefillParams& p, const StateGrid& sg, unsigned nblocks, hipStream_t stream, int steps) {
     if constexpr (STEPS < kMaxGroups) {
         if (steps == STEPS) {
-            hipLaunchKernelGGL((gdn_prefill_scan_kernel<STEPS>), dim3(nblocks), dim3(512), 0, stream, p, sg);
+            if (sg.plan)
+                hipLaunchKernelGGL((gdn_prefill_scan_kernel<STEPS, true>), dim3(nblocks), dim3(512), 0, stream, p, sg);
+            else
+                hipLaunchKernelGGL((gdn_prefill_scan_kernel<STEPS, false>), dim3(nblocks), dim3(512), 0, stream, p, sg);
             return gdn_host::check_launch("gdn_prefill_scan_kernel");
         }
         return launch_scan<STEPS + 1>(p, sg, nblocks, stream, steps);
     } else {
         return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: %d chunk groups", steps + 1);
+    }
+}
+
+// Chunk groups of packed sequences, balanced by length: the smallest group
+// length L (at least 4 chunks) for which sum_i min(16, ceil(n_i / L)) groups
+// fit `target` slots per head, n_i the chunks of sequence i (an empty
+// sequence keeps one group, which passes its state through).  Every group of
+// a sequence then has ceil(n_i / G_i) chunks (the last may have fewer), so the
+// longest chain is about L wherever the long sequences sit, instead of the
+// longest sequence over one group count shared by all.  One wave; writes the
+// StateGrid::plan table.  Requires nseq <= target <= kPlanCap.
+__global__ __launch_bounds__(64) void gdn_prefill_plan_kernel(const int32_t* __restrict__ cu, int nseq, int target,
+                                                              int32_t* __restrict__ tab) {
+    const int lane = threadIdx.x;
+    auto nchunks = [&](int i) { return (cu[i + 1] - cu[i] + kC - 1) / kC; };
+    auto gcount = [&](int n, int L) { return min(kMaxGroups, max(1, (n + L - 1) / L)); };
+    // Chunk counts of sequences lane + 64 u (nseq <= target <= kPlanCap = 256).
+    int nc[kPlanCap / 64];
+    int nmax = 0;
+#pragma unroll
+    for (int u = 0; u < kPlanCap / 64; ++u) {
+        const int i = lane + 64 * u;
+        nc[u] = i < nseq ? nchunks(i) : -1;
+        nmax = max(nmax, nc[u]);
+    }
+    for (int off = 32; off > 0; off >>= 1) nmax = max(nmax, __shfl_xor(nmax, off));
+    auto total = [&](int L) {
+        int t = 0;
+#pragma unroll
+        for (int u = 0; u < kPlanCap / 64; ++u) t += nc[u] >= 0 ? gcount(nc[u], L) : 0;
+        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+        return t;
+    };
+    int lo = 4, hi = max(4, nmax);  // total(hi) = nseq <= target
+    while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (total(mid) <= target)
+            hi = mid;
+        else
+            lo = mid + 1;
+    }
+    // Slots in sequence order: sequence i = lane + 64 u takes slots from the
+    // sum of G over the sequences before it (exclusive wave scans per u).
+    int base = 0, mbase = 0;
+#pragma unroll
+    for (int u = 0; u < kPlanCap / 64; ++u) {
+        const int i = lane + 64 * u;
+        const int G = nc[u] >= 0 ? gcount(nc[u], lo) : 0, M = G > 0 ? G - 1 : 0;
+        int x = G, y = M;  // inclusive scans
+        for (int off = 1; off < 64; off <<= 1) {
+            const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
+            if (lane >= off) {
+                x += xs;
+                y += ys;
+            }
+        }
+        const int first = base + x - G, mfirst = mbase + y - M;
+        if (i < nseq) {
+            tab[2 + 2 * i] = G;
+            tab[3 + 2 * i] = first;
+            for (int g = 0; g < G; ++g) {
+                tab[2 + 2 * nseq + first + g] = (i << 8) | g;
+                if (g < M) tab[2 + 2 * nseq + kPlanCap + mfirst + g] = (i << 8) | g;
+            }
+        }
+        base += __shfl(x, 63);
+        mbase += __shfl(y, 63);
+    }
+    if (lane == 0) {
+        tab[0] = base;
+        tab[1] = mbase;
     }
 }
 
@@ -1255,19 +1365,29 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
 }
 
 struct WsLayout {
-    size_t offT, offA, offG, offPsi, offPhi, total;
+    size_t offT, offA, offG, offPsi, offPhi, offPlan, total;
 };
 
-WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const StatePlan& sp) {
+// Packed sequences with chunk groups plan them per sequence on the device
+// (gdn_prefill_plan_kernel): target slots per head, at most 256 / (H nvg_out)
+// (one round of the output pass), which also bounds the group maps.
+bool planned_groups(const StatePlan& sp, bool varlen) { return varlen && sp.G > 1; }
+int plan_target(const StatePlan& sp, int H) { return std::max(1, 256 / (H * sp.nvg_out)); }
+
+WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const StatePlan& sp, bool varlen, int nseq) {
     const size_t ch = static_cast<size_t>(slots) * H;
+    const bool planned = planned_groups(sp, varlen);
     WsLayout L;
     L.offT = 0;
     L.offA = align256(L.offT + ch * kBytesT);
     L.offG = align256(L.offA + ch * kBytesA);
     L.offPsi = align256(L.offG + ch * kBytesG);
-    const size_t units = sp.G > 1 ? static_cast<size_t>(nheads) * sp.G : 0;
+    const size_t units = planned      ? static_cast<size_t>(H) * plan_target(sp, H)
+                         : sp.G > 1 ? static_cast<size_t>(nheads) * sp.G
+                                    : 0;
     L.offPhi = align256(L.offPsi + units * kDK * dv * 4);
-    L.total = align256(L.offPhi + units * kDK * kDK * 2);
+    L.offPlan = align256(L.offPhi + units * kDK * kDK * 2);
+    L.total = align256(L.offPlan + (planned ? (2 + 2 * static_cast<size_t>(nseq) + 2 * kPlanCap) * 4 : 0));
     return L;
 }
 
@@ -1314,7 +1434,8 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     using gdn_host::fail;
     const long long nheads = static_cast<long long>(nseq) * p.H;
     const StatePlan sp = plan_state(nheads, p.dv, nchunk_grid, exact);
-    const WsLayout L = ws_layout(slots, p.H, nheads, p.dv, sp);
+    const bool varlen = p.cu != nullptr;
+    const WsLayout L = ws_layout(slots, p.H, nheads, p.dv, sp, varlen, nseq);
     if (!workspace || ws_bytes < L.total)
         return fail(GDN_ERR_WORKSPACE, "prefill: workspace of %zu bytes given, %zu needed", ws_bytes, L.total);
     if (!gdn_host::aligned(workspace, 256))
@@ -1348,7 +1469,39 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     sg.nheads = static_cast<int>(nheads);
     sg.psi = reinterpret_cast<float*>(ws + L.offPsi);
     sg.phi = reinterpret_cast<uint16_t*>(ws + L.offPhi);
+    sg.nseq = nseq;
     int st;
+    if (planned_groups(sp, varlen)) {
+        // Per-sequence group counts, planned on the device from cu_seqlens.
+        const int target = plan_target(sp, p.H);
+        if (target > kPlanCap || nseq > target) return fail(GDN_ERR_UNSUPPORTED, "prefill: group plan");
+        int32_t* tab = reinterpret_cast<int32_t*>(ws + L.offPlan);
+        hipLaunchKernelGGL(gdn_prefill_plan_kernel, dim3(1), dim3(64), 0, stream, p.cu, nseq, target, tab);
+        st = gdn_host::check_launch("gdn_prefill_plan_kernel");
+        if (st != GDN_OK) return st;
+        sg.plan = tab;
+        const int map_cap = target - nseq;  // sum of G_i - 1
+        if (map_cap > 0) {
+            StateGrid sm = sg;
+            sm.nheads = p.H;  // grid: (head, map slot, column part)
+            sm.nvg = sp.nvg_map;
+            sm.ngroups_run = map_cap;
+            st = sp.NT_map == 4   ? launch_state<kModeMap, 4>(p, sm, sp.NW_map, stream)
+                 : sp.NT_map == 2 ? launch_state<kModeMap, 2>(p, sm, sp.NW_map, stream)
+                                  : launch_state<kModeMap, 1>(p, sm, sp.NW_map, stream);
+            if (st != GDN_OK) return st;
+            const long long nscan = nheads * (p.dv / 16);
+            if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
+            st = launch_scan<1>(p, sg, static_cast<unsigned>(nscan), stream, std::min(kMaxGroups - 1, map_cap));
+            if (st != GDN_OK) return st;
+        }
+        StateGrid so = sg;
+        so.nheads = p.H;  // grid: (head, slot, column part)
+        so.nvg = sp.nvg_out;
+        so.ngroups_run = target;
+        return sp.NT_out == 2 ? launch_state<kModeOut, 2>(p, so, sp.NW_out, stream)
+                              : launch_state<kModeOut, 1>(p, so, sp.NW_out, stream);
+    }
     if (sp.G > 1) {
         sg.nvg = sp.nvg_map;
         sg.ngroups_run = sp.G - 1;
@@ -1377,7 +1530,7 @@ size_t gdn_prefill_workspace_bytes(int B, int H, int T, int dk, int dv) {
     const long long nch = (T + kC - 1) / kC;
     const long long slots = static_cast<long long>(B) * nch;
     const long long nheads = static_cast<long long>(B) * H;
-    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, nch, false)).total;
+    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, nch, false), false, B).total;
 }
 
 size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int dk, int dv) {
@@ -1385,8 +1538,10 @@ size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int 
     if (num_seqs <= 0 || H <= 0 || T_total < 0 || dv <= 0) return 0;
     const long long slots = static_cast<long long>(T_total) / kC + num_seqs + 1;
     const long long nheads = static_cast<long long>(num_seqs) * H;
-    // The group count only grows with the longest sequence: size for T_total.
-    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, (T_total + kC - 1) / kC, false)).total;
+    // Whether chunk groups are used only grows with the longest sequence: size
+    // for T_total (the per-sequence plan then fits in H x 256 / (H nvg) maps).
+    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, (T_total + kC - 1) / kC, false), true, num_seqs)
+        .total;
 }
 
 }  // extern "C"
