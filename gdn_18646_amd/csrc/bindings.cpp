@@ -314,6 +314,59 @@ std::vector<Tensor> decode_conv_step(Tensor P, Tensor conv_w_qkv, Tensor cache_q
     return {q, k, v, a, b};
 }
 
+// Decode step, B <= 16: RMSNorm + projection + conv step + SiLU in one launch.
+// x [B, D]; caches and xn_hist (optional, [B, K - 1, D]) updated in place.
+std::vector<Tensor> decode_in_proj(Tensor x, Tensor gamma, double eps, Tensor W_qkvab, Tensor conv_w_qkv,
+                                   Tensor cache_q, Tensor cache_k, Tensor cache_v, std::optional<Tensor> xn_hist,
+                                   int64_t H, int64_t dk, int64_t dv) {
+    check_bf16(x, "x");
+    check_bf16(gamma, "gamma");
+    check_bf16(W_qkvab, "W_qkvab");
+    check_bf16(conv_w_qkv, "conv_w_qkv");
+    TORCH_CHECK(x.dim() == 2, "x must be [B, D]");
+    const int64_t B = x.size(0), D = x.size(1);
+    TORCH_CHECK(gamma.numel() == D, "gamma must have D entries");
+    TORCH_CHECK(W_qkvab.dim() == 2 && W_qkvab.size(0) == 2 * H * dk + H * dv + 2 * H && W_qkvab.size(1) == D,
+                "W_qkvab must be [2 H dk + H dv + 2 H, D]");
+    TORCH_CHECK(conv_w_qkv.dim() == 2 && conv_w_qkv.size(0) == 2 * H * dk + H * dv, "conv_w_qkv must be [2 H dk + H dv, K]");
+    const int64_t ck = conv_w_qkv.size(1);
+    check_bf16(cache_q, "cache_q");
+    check_bf16(cache_k, "cache_k");
+    check_bf16(cache_v, "cache_v");
+    TORCH_CHECK(cache_q.numel() == B * H * dk * (ck - 1) && cache_k.numel() == B * H * dk * (ck - 1) &&
+                    cache_v.numel() == B * H * dv * (ck - 1),
+                "conv caches must be [B, H d, K - 1]");
+    gdn_bf16_t* hist = nullptr;
+    if (xn_hist.has_value() && xn_hist->defined() && xn_hist->numel() > 0) {
+        check_bf16(*xn_hist, "xn_hist");
+        TORCH_CHECK(xn_hist->numel() == B * (ck - 1) * D, "xn_hist must be [B, K - 1, D]");
+        hist = bf_mut(*xn_hist);
+    }
+    const c10::DeviceGuard guard(x.device());
+    auto o = x.options();
+    auto q = at::empty({B, H, dk}, o), k = at::empty({B, H, dk}, o), v = at::empty({B, H, dv}, o);
+    auto a = at::empty({B, H}, o), b = at::empty({B, H}, o);
+    GDN_CHECK_STATUS(gdn_decode_in_proj_hip(bf(x), bf(gamma), static_cast<float>(eps), bf(W_qkvab), bf(conv_w_qkv),
+                                            bf_mut(cache_q), bf_mut(cache_k), bf_mut(cache_v), hist, bf_mut(q),
+                                            bf_mut(k), bf_mut(v), bf_mut(a), bf_mut(b), B, D, H, dk, dv, ck,
+                                            stream_of(x)),
+                     "decode_in_proj");
+    return {q, k, v, a, b};
+}
+
+// Decode step output projection: o [B, K] fp32 -> bf16(o) W^T [B, N] bf16.
+Tensor decode_out_proj(Tensor o, Tensor W) {
+    check_f32(o, "o");
+    check_bf16(W, "W");
+    TORCH_CHECK(o.dim() == 2 && W.dim() == 2 && W.size(1) == o.size(1), "o must be [B, K] and W [N, K]");
+    const int64_t B = o.size(0), K = o.size(1), N = W.size(0);
+    const c10::DeviceGuard guard(o.device());
+    auto y = at::empty({B, N}, o.options().dtype(at::kBFloat16));
+    GDN_CHECK_STATUS(gdn_decode_out_proj_hip(o.data_ptr<float>(), bf(W), bf_mut(y), B, K, N, stream_of(o)),
+                     "decode_out_proj");
+    return y;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -359,6 +412,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     ml.def("decode_conv_step", &decode_conv_step, "Decode conv step with projected-token caches (in place)",
            py::arg("P"), py::arg("conv_w_qkv"), py::arg("cache_q"), py::arg("cache_k"), py::arg("cache_v"),
            py::arg("H"), py::arg("dk"), py::arg("dv"));
+    ml.def("decode_in_proj", &decode_in_proj,
+           "Decode step (B <= 16): RMSNorm + q/k/v/a/b projection + conv step + SiLU; caches and xn_hist in place",
+           py::arg("x"), py::arg("gamma"), py::arg("eps"), py::arg("W_qkvab"), py::arg("conv_w_qkv"),
+           py::arg("cache_q"), py::arg("cache_k"), py::arg("cache_v"), py::arg("xn_hist") = py::none(),
+           py::arg("H"), py::arg("dk"), py::arg("dv"));
+    ml.def("decode_out_proj", &decode_out_proj, "Decode step output projection (B <= 16): bf16(o) W^T",
+           py::arg("o"), py::arg("W"));
 
     auto mj = m.def_submodule("proj", "Projection + causal conv + SiLU");
     mj.def("forward", &proj_forward, "Fused linear projection + causal depthwise conv1d + SiLU (bf16)",

@@ -2,6 +2,7 @@
 // gfx950 (CDNA4) only: wave64, bf16 MFMA 16x16x32, 160 KiB LDS per CU.
 #pragma once
 
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -49,6 +50,10 @@ __device__ __forceinline__ float softplus_f(float x) {
     return x > 20.f ? x : log1pf(expf(x));
 }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+// x * sigmoid(x) with the hardware exp2 and reciprocal (about 1 ulp each).
+__device__ __forceinline__ float silu_f(float x) {
+    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 // ---------------------------------------------------------------------------
 // Cross-lane sums over groups of 8 consecutive lanes, all DPP (no LDS).
@@ -91,6 +96,17 @@ __device__ __forceinline__ u32x2 pack4_bf16(const f32x4 v) {
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
+__device__ __forceinline__ u32x4 as_u32x4(const bf16x8 w) { return __builtin_bit_cast(u32x4, w); }
+
+// Compile-time loop: f(integral_constant<int, I>) for I in [B, E).  Keeps
+// register-array indices constant from the first optimisation pass on.
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& fn) {
+    if constexpr (B < E) {
+        fn(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(fn);
+    }
+}
 
 __device__ __forceinline__ bf16x8 pack8(const f32x4 lo, const f32x4 hi) {
     return as_bf16x8(u32x4{pack2_bf16(lo[0], lo[1]), pack2_bf16(lo[2], lo[3]), pack2_bf16(hi[0], hi[1]),
@@ -131,6 +147,19 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, lds_u8* 
 // Workgroup barrier for LDS producer/consumer hand-off: LDS writes of this
 // wave complete, then all waves meet.  (Async copies are covered by the
 // vmcnt wait that precedes it.)
+// Raw buffer resource over [base, base + bytes) (base uniform over the wave):
+// a load past the end returns zeros.  A buffer load addresses with the
+// resource (SGPRs), one 32-bit lane offset and a scalar offset, so a run of
+// loads in flight holds no 64-bit address per load in VGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // vmcnt(N) with the other counters open (gfx9 layout: vmcnt[3:0] | expcnt[6:4]

@@ -12,6 +12,18 @@
 // gdn_layer.py:43-55), fused with SiLU and the split into the decode kernel's
 // q/k/v/a/b layouts.  The reference's custom layer instead re-ran the fused
 // projection over a 4-token window of cached inputs (gdn_layer.py:58-69).
+//
+// gdn_decode_in_proj_hip / gdn_decode_out_proj_hip — a decode step's two
+// projections for up to 16 sequences, where the step is bound by streaming
+// the weights (25 MB and 8 MB at the layer's shape) and a library GEMM with
+// 4 rows reaches a fraction of HBM bandwidth.  Each workgroup owns 16 weight
+// rows and splits K over 8 waves, every lane loading its 16-byte B fragments
+// straight from memory; the rows of x (or o) are the MFMA A operand padded to
+// 16.  The in-projection also recomputes RMSNorm of x (same order of
+// operations as gdn_rmsnorm_kernel), keeps x_n W^T in fp32 for the conv step
+// + SiLU (as the prefill in-projection does), updates the conv caches and
+// the x_n history in place, and writes q/k/v/a/b in the decode kernel's
+// layouts; the out-projection rounds o to bf16 as it loads it.
 #include "gdn_common.hpp"
 #include "proj.hpp"
 
@@ -58,6 +70,272 @@ __global__ __launch_bounds__(256) void gdn_decode_conv_step_kernel(ConvStepParam
         y = pn;
     }
     p.dst[gi][static_cast<size_t>(b) * p.width[gi] + cc] = f2bf_bits(y);
+}
+
+
+// ---------------------------------------------------------------------------
+// Decode-step projections for B <= 16 (one token per sequence).
+//
+// A step streams the whole weight matrix once, so the kernel is built to keep
+// HBM busy: each lane's weight loads for all its K steps are issued at the
+// start and are the only data held in VGPRs while they fly (at most 128
+// VGPRs with MAXSTEPS <= 8, two 8-wave workgroups per CU: the in-projection's
+// ~390 workgroups are resident at once).  The in-projection's x and gamma go
+// to LDS by DMA before the weight loads, so RMSNorm runs while the weights
+// are still in flight.
+// ---------------------------------------------------------------------------
+constexpr int kSkM = 16;     // A-operand rows: sequences, zero beyond B
+constexpr int kSkWaves = 8;  // K split over the waves of a workgroup
+constexpr int kSkThreads = 64 * kSkWaves;
+constexpr int kSkMaxCols = 16;  // weight rows (output columns) per workgroup: 16, or 8 to spread small N
+constexpr int kSkStride = 32 * kSkWaves;  // K elements between a wave's consecutive steps
+constexpr int kSkCUs = 256;
+
+struct SkinnyParams {
+    const uint16_t* W;  // [N, K]
+    int B, K, N, cols;
+    const uint16_t* x;  // in-projection: x [B, K], normalised here
+    const uint16_t* gamma;
+    float eps;
+    const float* o;     // out-projection: o [B, K] fp32
+    uint16_t* y;        // out-projection: y [B, N]
+    const uint16_t* conv_w;  // in-projection epilogue: conv over the caches for groups 0..2
+    int conv_k;
+    uint16_t* cache[3];      // [B, width, conv_k - 1], oldest first, updated in place
+    uint16_t* dst[5];        // [B, width]
+    int col0[5];
+    int width[5];
+    uint16_t* xn_hist;       // [B, conv_k - 1, K] (nullable): shifted, x_n appended
+};
+
+// In-projection LDS (dynamic): x [B, K] bf16 rounded up to 1 KB plus a 1 KB
+// tail, then gamma (MAXSTEPS * 512 bytes).
+__host__ __device__ inline size_t skinny_x_bytes(int B, int K) { return (static_cast<size_t>(B) * K * 2 + 1023) / 1024 * 1024; }
+
+// A uniform value the optimiser cannot trace back to its kernel-argument load:
+// a select between such loads would otherwise become one vector load from the
+// argument block at a lane-selected offset, whose wait also waits for every
+// weight load in flight.
+template <typename T>
+__device__ __forceinline__ T opaque_sgpr(T v) {
+    asm("" : "+s"(v));
+    return v;
+}
+
+// MODE 0: in-projection, MODE 1: out-projection.  Wave w takes the 32-wide
+// K steps w, w + 8, w + 16, ...: nsteps of them.  All MAXSTEPS step slots run;
+// a slot past the wave's last step multiplies finite values by zero weights.
+template <int MODE, int MAXSTEPS>
+__global__ __launch_bounds__(kSkThreads)
+__attribute__((amdgpu_waves_per_eu(MAXSTEPS <= 8 ? 4 : 2, MAXSTEPS <= 8 ? 4 : 2)))
+void gdn_decode_skinny_kernel(SkinnyParams p) {
+    extern __shared__ __attribute__((aligned(1024))) unsigned char s_dyn[];
+    __shared__ float s_inv[kSkM];
+    __shared__ float s_red[kSkWaves][64][4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int n0 = blockIdx.x * p.cols;
+    const int ksteps = p.K / 32;
+    const int nsteps = (ksteps - wave + kSkWaves - 1) / kSkWaves;
+    const int kl = 32 * wave + 8 * g4;  // this lane's first K element
+    const bool arow = r16 < p.B;
+    // Lanes past B (A rows) or past the workgroup's columns (B columns) read a
+    // valid row, or zeros: they feed only MFMA output rows / columns that the
+    // epilogue discards.
+    const int arow_ld = min(r16, p.B - 1);
+    constexpr int kPast = 1 << 30;  // scalar offset past any buffer: the load returns zeros
+
+    lds_u8* const s_x = (lds_u8*)&s_dyn[0];
+    const uint32_t xbytes = static_cast<uint32_t>(p.B) * p.K * 2;
+    const uint32_t xregion = static_cast<uint32_t>(skinny_x_bytes(p.B, p.K));
+    lds_u8* const s_gamma = s_x + xregion + 1024;
+    if constexpr (MODE == 0) {
+        // x and gamma -> LDS by DMA, 1 KB per wave instruction (lanes past the
+        // end re-read the last 16 bytes); the 1 KB after x and the gamma slots
+        // past 2 K are zero-filled, so padded step slots read finite values.
+        for (uint32_t c = wave; c * 1024 < xregion; c += kSkWaves)
+            dma16(p.x, min(c * 1024 + 16 * lane, xbytes - 16), s_x + c * 1024);
+        if (wave == kSkWaves - 1) *reinterpret_cast<lds_u32x4*>(s_x + xregion + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+        const int gbytes = 2 * p.K;
+        if (wave < MAXSTEPS / 2) {
+            if (wave * 1024 < gbytes)
+                dma16(p.gamma, static_cast<uint32_t>(min(wave * 1024 + 16 * lane, gbytes - 16)), s_gamma + wave * 1024);
+            else
+                *reinterpret_cast<lds_u32x4*>(s_gamma + wave * 1024 + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+
+    // Weight rows n0 + lane % 16 (B operand): one buffer load per step slot
+    // (rows past N and slots past the last step read zeros).
+    const auto wrs = buffer_rsrc(p.W + static_cast<size_t>(min(n0, p.N)) * p.K,
+                                 static_cast<uint32_t>(max(0, min(p.cols, p.N - n0))) * p.K * 2);
+    const uint32_t wvoff = static_cast<uint32_t>(min(r16, p.cols - 1) * p.K + kl) * 2;
+    u32x4 bw[MAXSTEPS];
+#pragma unroll
+    for (int s = 0; s < MAXSTEPS; ++s) bw[s] = buffer_load16(wrs, wvoff, s < nsteps ? 2 * kSkStride * s : kPast);
+
+    bf16x8 af[MAXSTEPS];
+    const int er = tid >> 4, ec = tid & 15, en = n0 + ec;
+    const bool eown = tid < kSkM * kSkMaxCols && er < p.B && ec < p.cols && en < p.N;
+    int egi = 0;
+    float ws0 = 0.f, ws1 = 0.f, ws2 = 0.f, ws3 = 0.f, cs0 = 0.f, cs1 = 0.f, cs2 = 0.f;
+    uint16_t* ecache = nullptr;
+    const int nc = p.conv_k - 1, sh = 4 - p.conv_k;
+    if constexpr (MODE == 0) {
+        // The DMA completes before the MAXSTEPS weight loads issued after it.
+        // Barriers here order LDS only: a full __syncthreads() fence would
+        // also wait for the weight loads in flight.
+        wait_vm<MAXSTEPS>();
+        lds_barrier();
+        // RMSNorm statistics in gdn_rmsnorm_kernel's order (a lane sums its
+        // 16-byte chunks lane + 64 u, then a butterfly over the wave), so x_n
+        // equals that kernel's output bit for bit.
+        for (int m = wave; m < p.B; m += kSkWaves) {
+            float ss = 0.f;
+            for (int c = lane; c < p.K / 8; c += 64) {
+                float f[8];
+                unpack8(*reinterpret_cast<const lds_u32x4*>(s_x + (m * p.K + 8 * c) * 2), f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) s_inv[m] = 1.f / sqrtf(ss / static_cast<float>(p.K) + p.eps);
+        }
+
+        // Epilogue ownership: thread t < 256 computes output (row t / 16,
+        // column n0 + t % 16).  Its conv taps and cache window load now (from
+        // clamped, valid positions), right-aligned in four slots: slot 3 = the
+        // new token, slots 0..2 = the cached tokens, oldest first; slots before
+        // 4 - conv_k hold zero weight and zero input.
+        const int er_ld = min(er, p.B - 1), en_ld = min(en, p.N - 1);
+#pragma unroll
+        for (int q = 1; q < 5; ++q)
+            if (en_ld >= p.col0[q]) egi = q;
+        const int cgi = egi < 3 ? egi : 0;  // a/b columns read column 0's entries, unused
+        const int ccol = egi < 3 ? en_ld : 0;
+        const uint16_t* wrow = p.conv_w + static_cast<size_t>(ccol) * p.conv_k;
+        uint16_t* const cbase = cgi == 0 ? opaque_sgpr(p.cache[0]) : cgi == 1 ? opaque_sgpr(p.cache[1]) : opaque_sgpr(p.cache[2]);
+        const int cwidth = cgi == 0 ? opaque_sgpr(p.width[0]) : cgi == 1 ? opaque_sgpr(p.width[1]) : opaque_sgpr(p.width[2]);
+        const int ccol0 = cgi == 0 ? opaque_sgpr(p.col0[0]) : cgi == 1 ? opaque_sgpr(p.col0[1]) : opaque_sgpr(p.col0[2]);
+        ecache = cbase + (static_cast<size_t>(er_ld) * cwidth + (ccol - ccol0)) * nc;
+        const uint16_t* cread = nc > 0 ? ecache : wrow;  // conv_k == 1: no cache
+        const float t0 = bf2f(wrow[max(0 - sh, 0)]), t1 = bf2f(wrow[max(1 - sh, 0)]);
+        const float t2 = bf2f(wrow[max(2 - sh, 0)]), t3 = bf2f(wrow[3 - sh]);
+        const float u0 = bf2f(cread[max(0 - sh, 0)]), u1 = bf2f(cread[max(1 - sh, 0)]);
+        const float u2 = bf2f(cread[max(2 - sh, 0)]);
+        ws0 = sh <= 0 ? t0 : 0.f;
+        ws1 = sh <= 1 ? t1 : 0.f;
+        ws2 = sh <= 2 ? t2 : 0.f;
+        ws3 = t3;
+        cs0 = sh <= 0 ? u0 : 0.f;
+        cs1 = sh <= 1 ? u1 : 0.f;
+        cs2 = sh <= 2 ? u2 : 0.f;
+        // x_n history: workgroup b shifts and appends K step b (wave b % 8,
+        // slot b / 8); the grid has at least K / 32 workgroups (extra ones own
+        // no columns).  The entries it moves load now.
+        const int hstep = blockIdx.x;
+        const bool hown = p.xn_hist && nc > 0 && hstep < ksteps && wave == hstep % kSkWaves;
+        uint16_t* const hrow = p.xn_hist + static_cast<size_t>(arow_ld) * nc * p.K + 32 * hstep + 8 * g4;
+        // (unconditional loads, from x where there is nothing to move: a
+        // conditional one would merge registers across a branch and wait)
+        const u32x4 hold1 = *reinterpret_cast<const u32x4*>(hown && nc > 1 ? hrow + p.K : p.x);
+        const u32x4 hold2 = *reinterpret_cast<const u32x4*>(hown && nc > 2 ? hrow + 2 * p.K : p.x);
+        lds_barrier();
+
+        // A operand x_n = bf16((x * inv) * gamma), as gdn_rmsnorm_kernel.
+        const float inv = s_inv[arow_ld];
+        const lds_u8* xrow = s_x + (arow_ld * p.K + kl) * 2;
+#pragma unroll
+        for (int s = 0; s < MAXSTEPS; ++s) {
+            float f[8], gm[8];
+            unpack8(*reinterpret_cast<const lds_u32x4*>(xrow + 2 * kSkStride * s), f);
+            unpack8(*reinterpret_cast<const lds_u32x4*>(s_gamma + 2 * (kl + kSkStride * s)), gm);
+            af[s] = as_bf16x8(u32x4{pack2_bf16((f[0] * inv) * gm[0], (f[1] * inv) * gm[1]),
+                                    pack2_bf16((f[2] * inv) * gm[2], (f[3] * inv) * gm[3]),
+                                    pack2_bf16((f[4] * inv) * gm[4], (f[5] * inv) * gm[5]),
+                                    pack2_bf16((f[6] * inv) * gm[6], (f[7] * inv) * gm[7])});
+        }
+        if (hown && arow) {
+            const int hs = hstep / kSkWaves;
+            u32x4 xn = as_u32x4(af[0]);
+#pragma unroll
+            for (int s = 1; s < MAXSTEPS; ++s)
+                if (s == hs) xn = as_u32x4(af[s]);
+            if (nc > 1) *reinterpret_cast<u32x4*>(hrow) = hold1;
+            if (nc > 2) *reinterpret_cast<u32x4*>(hrow + static_cast<size_t>(p.K)) = hold2;
+            *reinterpret_cast<u32x4*>(hrow + static_cast<size_t>(nc - 1) * p.K) = xn;
+        }
+    } else {
+        const auto ors = buffer_rsrc(p.o, static_cast<uint32_t>(p.B) * p.K * 4);
+        const uint32_t ovoff = static_cast<uint32_t>(arow_ld * p.K + kl) * 4;
+#pragma unroll
+        for (int s = 0; s < MAXSTEPS; ++s) {
+            const int so = s < nsteps ? 4 * kSkStride * s : kPast;
+            af[s] = pack8(__builtin_bit_cast(f32x4, buffer_load16(ors, ovoff, so)),
+                          __builtin_bit_cast(f32x4, buffer_load16(ors, ovoff + 16, so)));
+        }
+    }
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < MAXSTEPS; ++s) acc = mfma16x16x32(af[s], as_bf16x8(bw[s]), acc);
+    // acc: column n0 + lane % 16, rows 4 (lane / 16) + i.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_red[wave][lane][i] = acc[i];
+    lds_barrier();
+    if (!eown) return;
+    float P = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSkWaves; ++w) P += s_red[w][(er >> 2) * 16 + ec][er & 3];
+    if constexpr (MODE == 1) {
+        p.y[static_cast<size_t>(er) * p.N + en] = f2bf_bits(P);
+    } else {
+        float y = P;
+        if (egi < 3) {
+            float sc = ws3 * P;
+            sc += ws0 * cs0;
+            sc += ws1 * cs1;
+            sc += ws2 * cs2;
+            // shift: entry e takes slot sh + e + 1, the last entry the new token
+            if (nc == 3) {
+                ecache[0] = f2bf_bits(cs1);
+                ecache[1] = f2bf_bits(cs2);
+            } else if (nc == 2) {
+                ecache[0] = f2bf_bits(cs2);
+            }
+            if (nc > 0) ecache[nc - 1] = f2bf_bits(P);
+            y = silu_f(sc);
+        }
+        uint16_t* dbase = opaque_sgpr(p.dst[0]);
+        int dw = opaque_sgpr(p.width[0]), dc = opaque_sgpr(p.col0[0]);
+#pragma unroll
+        for (int q = 1; q < 5; ++q)
+            if (egi == q) {
+                dbase = opaque_sgpr(p.dst[q]);
+                dw = opaque_sgpr(p.width[q]);
+                dc = opaque_sgpr(p.col0[q]);
+            }
+        dbase[static_cast<size_t>(er) * dw + (en - dc)] = f2bf_bits(y);
+    }
+}
+
+// Weight rows per workgroup: 16, or 8 when 16 would leave CUs idle.
+inline int skinny_cols(int N) { return (N + 15) / 16 >= kSkCUs ? 16 : 8; }
+
+template <int MODE>
+int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
+    p.cols = skinny_cols(p.N);
+    // the in-projection's grid also covers the K / 32 slices of the x_n history
+    const dim3 grid(max((p.N + p.cols - 1) / p.cols, MODE == 0 ? p.K / 32 : 0));
+    const bool small = p.K <= kSkStride * 8;
+    const size_t lds = MODE == 0 ? skinny_x_bytes(p.B, p.K) + 1024 + kSkStride * (small ? 8 : 16) * 2 : 0;
+    if (small)
+        hipLaunchKernelGGL((gdn_decode_skinny_kernel<MODE, 8>), grid, dim3(kSkThreads), lds, st, p);
+    else
+        hipLaunchKernelGGL((gdn_decode_skinny_kernel<MODE, 16>), grid, dim3(kSkThreads), lds, st, p);
+    return gdn_host::check_launch(who);
 }
 
 }  // namespace
@@ -138,4 +416,73 @@ extern "C" int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* c
     hipLaunchKernelGGL(gdn_decode_conv_step_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), p);
     return gdn_host::check_launch("gdn_decode_conv_step_kernel");
+}
+
+extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps,
+                                      const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q,
+                                      gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, gdn_bf16_t* xn_hist, gdn_bf16_t* q,
+                                      gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, int B, int D, int H,
+                                      int dk, int dv, int conv_k, void* stream) {
+    using gdn_host::aligned;
+    using gdn_host::fail;
+    if (B < 0 || D <= 0 || H <= 0 || dk <= 0 || dv <= 0)
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_in_proj: B=%d D=%d H=%d dk=%d dv=%d", B, D, H, dk, dv);
+    if (B > kSkM) return fail(GDN_ERR_UNSUPPORTED, "decode_in_proj: B=%d, at most %d sequences", B, kSkM);
+    if (D % 32 != 0 || D > kSkStride * 16)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_in_proj: D=%d must be a multiple of 32, at most %d", D,
+                    kSkStride * 16);
+    if (conv_k < 1 || conv_k > 4) return fail(GDN_ERR_UNSUPPORTED, "decode_in_proj: conv_k=%d must be in 1..4", conv_k);
+    if (B == 0) return GDN_OK;
+    if (!x || !gamma || !W_qkvab || !conv_w_qkv || !q || !k || !v || !a || !b ||
+        (conv_k > 1 && (!cache_q || !cache_k || !cache_v)))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_in_proj: null pointer argument");
+    if (!aligned(x, 16) || !aligned(gamma, 16) || !aligned(W_qkvab, 16))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_in_proj: x/gamma/W need 16-byte alignment");
+    SkinnyParams p = {};
+    p.W = W_qkvab;
+    p.B = B;
+    p.K = D;
+    const int Hk = H * dk, Hv = H * dv;
+    p.N = 2 * Hk + Hv + 2 * H;
+    p.x = x;
+    p.gamma = gamma;
+    p.eps = eps;
+    p.conv_w = conv_w_qkv;
+    p.conv_k = conv_k;
+    p.cache[0] = cache_q;
+    p.cache[1] = cache_k;
+    p.cache[2] = cache_v;
+    uint16_t* dst[5] = {q, k, v, a, b};
+    const int col0[5] = {0, Hk, 2 * Hk, 2 * Hk + Hv, 2 * Hk + Hv + H};
+    const int width[5] = {Hk, Hk, Hv, H, H};
+    for (int i = 0; i < 5; ++i) {
+        p.dst[i] = dst[i];
+        p.col0[i] = col0[i];
+        p.width[i] = width[i];
+    }
+    p.xn_hist = xn_hist;
+    return launch_skinny<0>(p, static_cast<hipStream_t>(stream), "gdn_decode_skinny_kernel<in>");
+}
+
+extern "C" int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W_o, gdn_bf16_t* y, int B, int K, int N,
+                                       void* stream) {
+    using gdn_host::aligned;
+    using gdn_host::fail;
+    if (B < 0 || K <= 0 || N <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: B=%d K=%d N=%d", B, K, N);
+    if (B > kSkM) return fail(GDN_ERR_UNSUPPORTED, "decode_out_proj: B=%d, at most %d sequences", B, kSkM);
+    if (K % 32 != 0 || K > kSkStride * 16)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_out_proj: K=%d must be a multiple of 32, at most %d", K,
+                    kSkStride * 16);
+    if (B == 0) return GDN_OK;
+    if (!o || !W_o || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: null pointer argument");
+    if (!aligned(o, 16) || !aligned(W_o, 16))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: o/W need 16-byte alignment");
+    SkinnyParams p = {};
+    p.W = W_o;
+    p.B = B;
+    p.K = K;
+    p.N = N;
+    p.o = o;
+    p.y = y;
+    return launch_skinny<1>(p, static_cast<hipStream_t>(stream), "gdn_decode_skinny_kernel<out>");
 }

@@ -218,21 +218,6 @@ __device__ __forceinline__ float tap_prev(float cur, float prev) {
     return __int_as_float(__builtin_amdgcn_update_dpp(rot, __float_as_int(cur), 0x110 + K, 0xf, 0xf, false));
 }
 
-// x * sigmoid(x) with the hardware exp2 and reciprocal (about 1 ulp each).
-__device__ __forceinline__ float silu_f(float x) {
-    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
-}
-
-// Compile-time loop: f(integral_constant<int, I>) for I in [B, E).  Keeps
-// register-array indices constant from the first optimisation pass on.
-template <int B, int E, typename Fn>
-__device__ __forceinline__ void static_for(Fn&& fn) {
-    if constexpr (B < E) {
-        fn(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(fn);
-    }
-}
-
 // The group holding column c, by compare-and-select over constant indices
 // (indexing the parameter block with a runtime index would copy it to
 // private memory).

@@ -111,6 +111,10 @@ class GDNLayerCustom:
         self.dt_bias_scalar = float(dtb.reshape(-1)[0].item()) if dtb.numel() == 1 else None
         self.dt_bias_vec = _dt_bias_for_decode(dtb, self.H).float().contiguous()
         self.W_o = w['W_o'].contiguous()
+        self.gamma = w['norm_gamma'].contiguous()
+        # One-launch input and output projections of a decode step (B <= 16).
+        self.fused_decode = (self.D % 32 == 0 and self.D <= 4096 and (self.H * self.DV) % 32 == 0
+                             and self.H * self.DV <= 4096 and 1 <= self.CK <= 4)
 
     def init_decode_state(self, B, device=None):
         return _zero_decode_state(self.w, B, device=device)
@@ -166,21 +170,33 @@ class GDNLayerCustom:
         Dd, Hh, dk, dv = self.D, self.H, self.DK, self.DV
         if state is None:
             state = self.init_decode_state(B, device=x.device)
-        xn = self._rmsnorm(x.reshape(B, Dd))
-        P = xn @ self.W_qkvab.T
         if inplace:
             cq, ck, cv, S_out = state['conv_q'], state['conv_k'], state['conv_v'], state['recurrent']
         else:
             cq, ck, cv = (state[n].clone() for n in ('conv_q', 'conv_k', 'conv_v'))
             S_out = torch.empty_like(state['recurrent'])
-        q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv)
+        fused = self.fused_decode and B <= 16
+        if fused:
+            # RMSNorm, projection, conv step and the x_n history in one launch
+            xn_hist = state['xn'] if inplace else state['xn'].clone()
+            q, k, v, a, b = self._layer.decode_in_proj(x.reshape(B, Dd).contiguous(), self.gamma, 1e-6,
+                                                       self.W_qkvab, self.conv_qkv, cq, ck, cv, xn_hist,
+                                                       Hh, dk, dv)
+        else:
+            xn = self._rmsnorm(x.reshape(B, Dd))
+            P = xn @ self.W_qkvab.T
+            q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv)
+            xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
+            if inplace:
+                state['xn'].copy_(xn_hist)  # same tensor, so a captured step stays valid
         o = torch.empty(B, Hh, dv, dtype=torch.float32, device=x.device)
         self.exts['decode'].forward(q, k, v, a, b, self.A_log, self.dt_bias_vec, state['recurrent'], self.scale,
                                     o, S_out)
-        y = o.to(x.dtype).reshape(B, 1, Hh * dv) @ self.W_o.T
-        xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
+        if fused:
+            y = self._layer.decode_out_proj(o.reshape(B, Hh * dv), self.W_o).reshape(B, 1, Dd)
+        else:
+            y = o.to(x.dtype).reshape(B, 1, Hh * dv) @ self.W_o.T
         if inplace:
-            state['xn'].copy_(xn_hist)  # same tensor, so a captured step stays valid
             return y, state
         return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist.contiguous())
 

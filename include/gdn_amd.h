@@ -19,6 +19,9 @@
  *   gdn_proj_conv_silu_hip    <- fused_proj_conv_silu, kernels/fused_proj_conv_silu.cu:298-355
  *   gdn_in_proj_hip           <- GDNLayerCustom.forward's projections, gdn_layer.py:240-252
  *   gdn_decode_conv_step_hip  <- _decode_conv_step / _decode_fused_proj_step, gdn_layer.py:43-69
+ *   gdn_decode_in_proj_hip    <- GDNLayerCustom.decode's RMSNorm, projections and conv step,
+ *                                gdn_layer.py:280-299 (with 43-69)
+ *   gdn_decode_out_proj_hip   <- GDNLayerCustom.decode's output projection, gdn_layer.py:309
  */
 #ifndef GDN_AMD_H
 #define GDN_AMD_H
@@ -200,6 +203,33 @@ int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* conv_w_qkv,
                              gdn_bf16_t* cache_q, gdn_bf16_t* cache_k, gdn_bf16_t* cache_v,
                              gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
                              int B, int H, int dk, int dv, int conv_k, void* stream);
+
+/*
+ * One decode step's input side for B <= 16 sequences: x_n = RMSNorm(x)
+ * (x [B, D] bf16, gamma [D], eps; the same numbers as gdn_rmsnorm_hip),
+ * P = x_n W_qkvab^T kept in fp32, then the conv step of
+ * gdn_decode_conv_step_hip on P (conv caches updated in place; they receive
+ * bf16(P)) and SiLU.  Outputs q, k [B, H, dk]; v [B, H, dv]; a, b [B, H].
+ * xn_hist [B, conv_k - 1, D] (NULL = skipped) is shifted one token and x_n
+ * appended, in place.  D % 32 == 0, D <= 4096, conv_k in 1..4.  Caches and
+ * xn_hist must not alias the outputs.
+ * Replaces GDNLayerCustom.decode's rmsnorm, projection GEMM and conv step
+ * (gdn_layer.py:280-299 and 43-69).
+ */
+int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps, const gdn_bf16_t* W_qkvab,
+                           const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q, gdn_bf16_t* cache_k,
+                           gdn_bf16_t* cache_v, gdn_bf16_t* xn_hist, gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v,
+                           gdn_bf16_t* a, gdn_bf16_t* b, int B, int D, int H, int dk, int dv, int conv_k,
+                           void* stream);
+
+/*
+ * y [B, N] bf16 = bf16(o) W^T for o [B, K] fp32 (the decode kernel's output,
+ * rounded to bf16 as the reference's o.to(bf16)), W [N, K] bf16, fp32
+ * accumulation.  B <= 16, K % 32 == 0, K <= 4096.
+ * Replaces GDNLayerCustom.decode's output projection (gdn_layer.py:309).
+ */
+int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W, gdn_bf16_t* y, int B, int K, int N,
+                            void* stream);
 
 #ifdef __cplusplus
 }

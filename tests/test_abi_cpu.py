@@ -92,6 +92,27 @@ def test_support_validation_errors():
         abi.call("gdn_proj_conv_silu_hip", FAKE, FAKE, FAKE, FAKE, 1, 8, 128, 64, 5, None)
 
 
+def test_decode_projection_validation_errors():
+    in_args = lambda B, D, ck: ([FAKE, FAKE, 1e-6] + [FAKE] * 11 + [B, D, 2, 128, 128, ck, None])
+    with pytest.raises(GdnError, match="UNSUPPORTED.*B=17"):
+        abi.call("gdn_decode_in_proj_hip", *in_args(17, 2048, 4))
+    with pytest.raises(GdnError, match="UNSUPPORTED.*D=100"):
+        abi.call("gdn_decode_in_proj_hip", *in_args(4, 100, 4))
+    with pytest.raises(GdnError, match="UNSUPPORTED.*D=8192"):
+        abi.call("gdn_decode_in_proj_hip", *in_args(4, 8192, 4))
+    with pytest.raises(GdnError, match="conv_k"):
+        abi.call("gdn_decode_in_proj_hip", *in_args(4, 2048, 5))
+    with pytest.raises(GdnError, match="INVALID_ARGUMENT.*null"):
+        abi.call("gdn_decode_in_proj_hip", None, *in_args(4, 2048, 4)[1:])
+    abi.call("gdn_decode_in_proj_hip", *in_args(0, 2048, 4))  # B == 0: no-op
+    with pytest.raises(GdnError, match="UNSUPPORTED.*B=17"):
+        abi.call("gdn_decode_out_proj_hip", FAKE, FAKE, FAKE, 17, 2048, 2048, None)
+    with pytest.raises(GdnError, match="UNSUPPORTED.*K=2050"):
+        abi.call("gdn_decode_out_proj_hip", FAKE, FAKE, FAKE, 4, 2050, 2048, None)
+    with pytest.raises(GdnError, match="alignment"):
+        abi.call("gdn_decode_out_proj_hip", FAKE + 4, FAKE, FAKE, 4, 2048, 2048, None)
+
+
 def test_binding_module_api_matches_reference():
     """Module names, attrs and signatures of the reference's pybind modules."""
     exts = compile_kernels()

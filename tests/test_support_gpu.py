@@ -6,7 +6,8 @@ torch.nn.RMSNorm.  The projection kernel keeps P in fp32 before the conv (as the
 reference kernel does), so it is held to the fp32 composition within bf16
 output tolerance, and to the reference's bf16-rounded oracle with the
 reference test's max-error bound (tests/test_fused_proj_conv_silu.py:55-59)
-plus a relative term.
+plus a relative term.  The decode-step projections (one token, B <= 16) are
+held to the same fp32 compositions, with x_n bit-equal to the RMSNorm kernel's.
 """
 
 import pytest
@@ -143,3 +144,46 @@ def test_in_proj_matches_fp32_composition(dev, H, B, T, with_cache):
         assert_out_close(y.cpu(), r, what=name)
     for name, y, r in zip(("cache_q", "cache_k", "cache_v"), got[5:], want[1]):
         assert_out_close(y.cpu(), r, atol=1e-2, rtol=1e-2, what=name)
+
+
+# Decode-step projections (B <= 16).  D = 96 leaves five of the eight waves
+# without K steps; D = 2048 / H = 16 is the layer's shape.
+@pytest.mark.parametrize("B", [1, 4, 16])
+@pytest.mark.parametrize("H,dk,dv,D,ck", [(2, 32, 16, 128, 4), (4, 32, 16, 96, 3), (2, 32, 16, 256, 2),
+                                          (16, 128, 128, 2048, 4)])
+def test_decode_in_proj_matches_composition(exts, dev, B, H, dk, dv, D, ck):
+    from gdn_18646_amd import native_extension
+    lay = native_extension().layer
+    g = torch.Generator().manual_seed(B * 1000 + D + ck)
+    Dout = 2 * H * dk + H * dv + 2 * H
+    x = torch.randn(B, D, generator=g).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    W = (torch.randn(Dout, D, generator=g) * D ** -0.5).bfloat16()
+    cw = (torch.randn(Dout - 2 * H, ck, generator=g) * 0.5).bfloat16()
+    caches = [torch.randn(B, H * d, ck - 1, generator=g).bfloat16() for d in (dk, dk, dv)]
+    hist = torch.randn(B, ck - 1, D, generator=g).bfloat16()
+    # x_n is the RMSNorm kernel's output bit for bit
+    xn = exts["rmsnorm"].forward(x.to(dev), gamma.to(dev), 1e-6, 256, 2).cpu()
+    assert_out_close(xn, ref_rmsnorm(x, gamma), what="rmsnorm")
+    want, want_cache = _in_proj_expected(xn.reshape(B, 1, D), W, cw, H, dk, dv, caches)
+    cd, hd = [c.to(dev) for c in caches], hist.to(dev)
+    got = lay.decode_in_proj(x.to(dev), gamma.to(dev), 1e-6, W.to(dev), cw.to(dev), *cd, hd, H, dk, dv)
+    for name, y, r in zip("qkvab", got, want):
+        assert_out_close(y.cpu(), r.reshape(y.shape), what=name)
+    for name, y, r in zip(("cache_q", "cache_k", "cache_v"), cd, want_cache):
+        assert_out_close(y.cpu(), r, atol=1e-2, rtol=1e-2, what=name)
+    assert torch.equal(hd.cpu(), torch.cat([hist[:, 1:], xn[:, None]], 1)), "x_n history"
+
+
+@pytest.mark.parametrize("B,K,N", [(1, 2048, 2048), (4, 2048, 2048), (16, 128, 256), (3, 96, 40), (7, 4096, 100)])
+def test_decode_out_proj_matches_composition(dev, B, K, N):
+    from gdn_18646_amd import native_extension
+    lay = native_extension().layer
+    g = torch.Generator().manual_seed(B + K + N)
+    o = torch.randn(B, K, generator=g)
+    W = (torch.randn(N, K, generator=g) * K ** -0.5).bfloat16()
+    want = (o.bfloat16().float() @ W.float().T).bfloat16()
+    assert_out_close(lay.decode_out_proj(o.to(dev), W.to(dev)).cpu(), want, what="out proj")
+    with pytest.raises(RuntimeError, match="B=17"):
+        lay.decode_out_proj(torch.zeros(17, K, device=dev), W.to(dev))
+
