@@ -150,7 +150,12 @@ extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gd
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 8) || !aligned(S_in, 16) ||
         !aligned(S_out, 16) || !aligned(o, 16))
         return fail(GDN_ERR_INVALID_ARGUMENT, "decode: q/k/S/o need 16-byte, v 8-byte alignment");
-    const int cw = dv % 128 == 0 ? 128 : (dv % 64 == 0 ? 64 : 32);
+    // Column slice: the widest of 128 / 64 / 32 dividing dv, halved while the
+    // grid would leave CUs idle (a small batch splits each head's columns
+    // over more workgroups; columns of the state update independently).
+    constexpr long long kCUs = 256;
+    int cw = dv % 128 == 0 ? 128 : (dv % 64 == 0 ? 64 : 32);
+    while (cw > 32 && static_cast<long long>(B) * H * (dv / cw) < kCUs) cw /= 2;
     const long long nwg_ll = static_cast<long long>(B) * H * (dv / cw);
     if (nwg_ll > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "decode: grid too large");
     const dim3 grid(static_cast<unsigned>(nwg_ll)), block(kWave * kWavesPerWG);
