@@ -147,10 +147,11 @@ def test_in_proj_matches_fp32_composition(dev, H, B, T, with_cache):
 
 
 # Decode-step projections (B <= 16).  D = 96 leaves five of the eight waves
-# without K steps; D = 2048 / H = 16 is the layer's shape.
+# without K steps; D = 2048 / H = 16 is the layer's shape; D = 4096 runs the
+# 16-step variant (x for 16 rows fills 128 KiB of LDS).
 @pytest.mark.parametrize("B", [1, 4, 16])
 @pytest.mark.parametrize("H,dk,dv,D,ck", [(2, 32, 16, 128, 4), (4, 32, 16, 96, 3), (2, 32, 16, 256, 2),
-                                          (16, 128, 128, 2048, 4)])
+                                          (16, 128, 128, 2048, 4), (2, 32, 16, 4096, 4)])
 def test_decode_in_proj_matches_composition(exts, dev, B, H, dk, dv, D, ck):
     from gdn_18646_amd import native_extension
     lay = native_extension().layer
