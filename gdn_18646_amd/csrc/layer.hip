@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void gdn_decode_conv_step_kernel(ConvStepParam
 // to LDS by DMA before the weight loads, so RMSNorm runs while the weights
 // are still in flight.
 // ---------------------------------------------------------------------------
-constexpr int kSkM = 16;     // A-operand rows: sequences, zero beyond B
+constexpr int kSkM = 16;     // A-operand rows: sequences (rows past B repeat row B - 1, outputs discarded)
 constexpr int kSkWaves = 8;  // K split over the waves of a workgroup
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkMaxCols = 16;  // weight rows (output columns) per workgroup: 16, or 8 to spread small N

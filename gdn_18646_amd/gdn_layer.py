@@ -136,8 +136,8 @@ class GDNLayerCustom:
             raise ValueError("prefill takes a scalar dt_bias (as the reference kernel)")
         B, T, _ = x.shape
         Dd, Hh, dk, dv = self.D, self.H, self.DK, self.DV
-        if mask is None:
-            mask = torch.ones(B, T, dtype=torch.float32, device=x.device)
+        if mask is None:  # empty = every token kept (no fill kernel)
+            mask = torch.empty(0, dtype=torch.float32, device=x.device)
         xn = self._rmsnorm(x.reshape(B * T, Dd)).reshape(B, T, Dd)
         st = state or {}
         outs = self._layer.in_proj(xn, self.W_qkvab, self.conv_qkv, Hh, dk, dv,
