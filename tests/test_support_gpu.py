@@ -148,10 +148,11 @@ def test_in_proj_matches_fp32_composition(dev, H, B, T, with_cache):
 
 # Decode-step projections (B <= 16).  D = 96 leaves five of the eight waves
 # without K steps; D = 2048 / H = 16 is the layer's shape; D = 4096 runs the
-# 16-step variant (x for 16 rows fills 128 KiB of LDS).
+# 16-step variant (x for 16 rows fills 128 KiB of LDS); conv width 1 has no
+# cache and no x_n history.
 @pytest.mark.parametrize("B", [1, 4, 16])
 @pytest.mark.parametrize("H,dk,dv,D,ck", [(2, 32, 16, 128, 4), (4, 32, 16, 96, 3), (2, 32, 16, 256, 2),
-                                          (16, 128, 128, 2048, 4), (2, 32, 16, 4096, 4)])
+                                          (16, 128, 128, 2048, 4), (2, 32, 16, 4096, 4), (2, 32, 16, 128, 1)])
 def test_decode_in_proj_matches_composition(exts, dev, B, H, dk, dv, D, ck):
     from gdn_18646_amd import native_extension
     lay = native_extension().layer
@@ -171,6 +172,8 @@ def test_decode_in_proj_matches_composition(exts, dev, B, H, dk, dv, D, ck):
     got = lay.decode_in_proj(x.to(dev), gamma.to(dev), 1e-6, W.to(dev), cw.to(dev), *cd, hd, H, dk, dv)
     for name, y, r in zip("qkvab", got, want):
         assert_out_close(y.cpu(), r.reshape(y.shape), what=name)
+    if ck == 1:
+        return
     for name, y, r in zip(("cache_q", "cache_k", "cache_v"), cd, want_cache):
         assert_out_close(y.cpu(), r, atol=1e-2, rtol=1e-2, what=name)
     assert torch.equal(hd.cpu(), torch.cat([hist[:, 1:], xn[:, None]], 1)), "x_n history"
