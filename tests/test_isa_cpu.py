@@ -1,0 +1,52 @@
+"""ISA checks of the decode-step in-projection (gdn_decode_skinny_kernel<0, *>)
+in gdn_18646_amd/csrc/layer.hip, on the CPU (hipcc cross-compiles gfx950).
+
+The kernel copies x and gamma to LDS with global_load_lds, then issues its
+MAXSTEPS weight loads, then waits with vmcnt(MAXSTEPS): vector memory
+operations retire in issue order, so that wait covers the LDS copies only if
+exactly MAXSTEPS vector memory operations sit between the last copy and the
+wait.  A compiler that moved another load (or a spill) into that window would
+let RMSNorm read LDS before the copy lands; this test fails first.
+"""
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+HIPCC = "/opt/rocm/bin/hipcc"
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "gdn_18646_amd", "csrc", "layer.hip")
+
+VMEM = re.compile(r"^\s*(buffer|global|scratch|flat)_(load|store|atomic)")
+
+
+@pytest.fixture(scope="module")
+def layer_asm(tmp_path_factory):
+    if not shutil.which(HIPCC):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa") / "layer.s"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", SRC, "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    return out.read_text()
+
+
+def _function(asm, symbol):
+    start = asm.index(f"\n{symbol}:")
+    return asm[start:asm.index("s_endpgm", start)].splitlines()
+
+
+@pytest.mark.parametrize("maxsteps", [8, 16])
+def test_in_proj_dma_wait_covers_only_the_weight_loads(layer_asm, maxsteps):
+    sym = f"_ZN12_GLOBAL__N_124gdn_decode_skinny_kernelILi0ELi{maxsteps}EEEvNS_12SkinnyParamsE"
+    body = _function(layer_asm, sym)
+    last_dma = max(i for i, ln in enumerate(body) if "global_load_lds_dwordx4" in ln)
+    wait = next(i for i in range(last_dma, len(body)) if re.search(r"s_waitcnt vmcnt\(\d+\)", body[i]))
+    n = int(re.search(r"vmcnt\((\d+)\)", body[wait]).group(1))
+    between = [ln.strip() for ln in body[last_dma + 1:wait] if VMEM.match(ln)]
+    assert n == maxsteps, f"first wait after the copies is vmcnt({n}), expected vmcnt({maxsteps})"
+    assert len(between) == maxsteps and all(ln.startswith("buffer_load_dwordx4") for ln in between), between
+    assert not any("scratch_" in ln for ln in body), "the kernel spills"
