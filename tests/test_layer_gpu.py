@@ -71,6 +71,21 @@ def test_layer_decode_matches_prefill(dev, inplace):
     assert_out_close(torch.cat(ys, 1), y_pre, what="decode vs prefill")
 
 
+def test_layer_decode_above_16_sequences_matches_prefill(dev):
+    """B > 16 takes the unfused decode step (RMSNorm, library GEMM, conv-step
+    kernel, library GEMM); it must agree with one prefill too."""
+    _, w = _weights(dev, seed=9)
+    layer = GDNLayerCustom(w)
+    x = torch.randn(20, 24, 256, generator=torch.Generator().manual_seed(10)).bfloat16().to(dev)
+    y_pre = layer.forward(x)
+    st = layer.init_decode_state(20)
+    ys = []
+    for t in range(24):
+        y_t, st = layer.decode(x[:, t:t + 1], st, inplace=True)
+        ys.append(y_t)
+    assert_out_close(torch.cat(ys, 1), y_pre, what="decode (B=20) vs prefill")
+
+
 def test_prefill_hands_off_to_decode(dev):
     """forward(x[:t], return_state) then decode tokens t.. == forward(x) (cache hand-off)."""
     _, w = _weights(dev, seed=6)
