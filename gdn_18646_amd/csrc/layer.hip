@@ -144,7 +144,9 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
     // valid row, or zeros: they feed only MFMA output rows / columns that the
     // epilogue discards.
     const int arow_ld = min(r16, p.B - 1);
-    constexpr int kPast = 1 << 30;  // scalar offset past any buffer: the load returns zeros
+    // Lane offset past any buffer: the range check (which always covers the
+    // lane offset) turns the load into zeros.
+    constexpr uint32_t kPast = 0x80000000u;
 
     lds_u8* const s_x = (lds_u8*)&s_dyn[0];
     const uint32_t xbytes = static_cast<uint32_t>(p.B) * p.K * 2;
@@ -173,7 +175,7 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
     const uint32_t wvoff = static_cast<uint32_t>(min(r16, p.cols - 1) * p.K + kl) * 2;
     u32x4 bw[MAXSTEPS];
 #pragma unroll
-    for (int s = 0; s < MAXSTEPS; ++s) bw[s] = buffer_load16(wrs, wvoff, s < nsteps ? 2 * kSkStride * s : kPast);
+    for (int s = 0; s < MAXSTEPS; ++s) bw[s] = buffer_load16(wrs, s < nsteps ? wvoff : kPast, 2 * kSkStride * s);
 
     bf16x8 af[MAXSTEPS];
     const int er = tid >> 4, ec = tid & 15, en = n0 + ec;
@@ -272,9 +274,9 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
         const uint32_t ovoff = static_cast<uint32_t>(arow_ld * p.K + kl) * 4;
 #pragma unroll
         for (int s = 0; s < MAXSTEPS; ++s) {
-            const int so = s < nsteps ? 4 * kSkStride * s : kPast;
-            af[s] = pack8(__builtin_bit_cast(f32x4, buffer_load16(ors, ovoff, so)),
-                          __builtin_bit_cast(f32x4, buffer_load16(ors, ovoff + 16, so)));
+            const uint32_t vo = s < nsteps ? ovoff : kPast;
+            af[s] = pack8(__builtin_bit_cast(f32x4, buffer_load16(ors, vo, 4 * kSkStride * s)),
+                          __builtin_bit_cast(f32x4, buffer_load16(ors, vo + 16, 4 * kSkStride * s)));
         }
     }
 
