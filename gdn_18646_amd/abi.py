@@ -27,6 +27,8 @@ SIGNATURES = {
                              _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "gdn_prefill_tm_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,
                                 _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "gdn_prefill_noalloc_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,
+                                     _I, _I, _I, _I, _I, _P]),
     "gdn_prefill_intra_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,
                                    _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "gdn_prefill_state_hip": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, _P, _F, _P, _P,

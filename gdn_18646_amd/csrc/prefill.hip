@@ -38,6 +38,7 @@
 //   rho(r,g,i) = 32(r/2) + 8g + 4(r%2) + i          state row held in
 //                accumulator tile r, slot i, of lane group g
 #include <algorithm>
+#include <mutex>
 
 #include "gdn_common.hpp"
 
@@ -1637,6 +1638,61 @@ int gdn_prefill_state_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf
                           int T, int dk, int dv, void* workspace, size_t workspace_bytes, void* stream) {
     return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
                          dv, workspace, workspace_bytes, stream, 2);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// No-allocation prefill: the workspace is a static device array, one copy per
+// GPU (each device that loads this code object holds it until the process
+// ends).  Its device address is looked up once per device, with that device
+// current, on the first call there; host code uses only that address (the
+// array's own name is a host-side stand-in, not a device pointer).  Nothing in
+// the workspace has to start zeroed: every chunk slot and group map that a
+// kernel reads was written earlier in the same call.  Calls that overlap on
+// one GPU (e.g. on two streams) share the array and race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = static_cast<size_t>(GDN_PREFILL_NOALLOC_MAX_BYTES);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+}  // namespace
+
+extern "C" {
+
+int gdn_prefill_noalloc_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                            const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                            const float* state_in, float scale, gdn_bf16_t* out, float* state_out, int B, int H,
+                            int T, int dk, int dv, void* stream) {
+    using gdn_host::fail;
+    // Sizes first: a request that cannot fit is refused before any HIP call.
+    const int st = check_common("prefill_noalloc", H, dk, dv);
+    if (st != GDN_OK) return st;
+    if (B < 0 || T < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "prefill_noalloc: B=%d T=%d", B, T);
+    const size_t need = gdn_prefill_workspace_bytes(B, H, T, dk, dv);
+    if (need > kScratchBytes)
+        return fail(GDN_ERR_WORKSPACE,
+                    "prefill_noalloc: B=%d H=%d T=%d dv=%d needs %zu bytes of scratch, the static buffer holds %zu "
+                    "(use gdn_prefill_hip with a caller workspace)",
+                    B, H, T, dv, need, kScratchBytes);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(GDN_ERR_HIP, "prefill_noalloc: hipGetDevice failed");
+    if (dev < 0 || dev >= kMaxDevices) return fail(GDN_ERR_UNSUPPORTED, "prefill_noalloc: device %d", dev);
+    ScratchSlot& s = g_scratch[dev];
+    std::call_once(s.once, [&s]() { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
+    if (s.err != hipSuccess || !s.ptr)
+        return fail(GDN_ERR_HIP, "prefill_noalloc: scratch address lookup failed: %s", hipGetErrorString(s.err));
+    return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
+                         dv, s.ptr, kScratchBytes, stream, 3);
 }
 
 int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,

@@ -12,6 +12,8 @@
  *   gdn_decode_hip            <- extern "C" gdn_decode_cuda, kernels/decode.cu:131-162
  *                                (and gdn_decode_forward, kernels/decode.cu:172-214)
  *   gdn_prefill_hip           <- gdn_prefill, kernels/prefill_chunked.cu:422-504
+ *   gdn_prefill_noalloc_hip   <- no reference counterpart (gdn_prefill_hip with a static
+ *                                scratch buffer, for callers that cannot allocate)
  *   gdn_prefill_varlen_hip    <- no reference counterpart (packed cu_seqlens prefill);
  *                                semantics = gdn_prefill per sequence
  *   gdn_rmsnorm_hip           <- rmsnorm_forward_impl / launch_rmsnorm,
@@ -107,6 +109,29 @@ int gdn_prefill_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_
                        gdn_bf16_t* out, float* state_out,
                        int B, int H, int T, int dk, int dv,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * gdn_prefill_hip without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.
+ * The per-chunk intermediates go to a static device buffer of
+ * GDN_PREFILL_NOALLOC_MAX_BYTES that the library holds per GPU until the
+ * process ends; the call allocates nothing.  A shape whose
+ * gdn_prefill_workspace_bytes() exceeds that size is refused with
+ * GDN_ERR_WORKSPACE before any HIP call (e.g. B=1, H=16, T=8192, dk=dv=128
+ * needs 54 MiB and fits; B=4, H=16, T=4096 needs 84 MiB and does not).
+ * All calls on one GPU share the buffer: calls that overlap on one GPU (two
+ * streams, two threads) race, so serialise them.  Nothing in it needs to
+ * start zeroed.  Outputs are bit-identical to gdn_prefill_hip's.
+ */
+#define GDN_PREFILL_NOALLOC_MAX_BYTES (64u << 20)
+
+int gdn_prefill_noalloc_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                            const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                            const gdn_bf16_t* b_logits, const float* mask,
+                            const float* state_in, float scale,
+                            gdn_bf16_t* out, float* state_out,
+                            int B, int H, int T, int dk, int dv, void* stream);
 
 /*
  * The two phases of gdn_prefill_hip, same arguments, for callers that overlap

@@ -55,6 +55,16 @@ def test_host_functions():
 FAKE = 4096  # non-null, 16-byte aligned; validation fails before it is ever dereferenced
 
 
+def test_prefill_noalloc_refuses_oversized_shape():
+    """The static scratch limit is checked before any HIP call (none runs here)."""
+    with pytest.raises(GdnError, match="WORKSPACE.*static buffer"):
+        abi.call("gdn_prefill_noalloc_hip", *([FAKE] * 5), 0.0, FAKE, FAKE, None, 0.0, FAKE, FAKE,
+                 4, 16, 4096, 128, 128, None)
+    with pytest.raises(GdnError, match="UNSUPPORTED.*dk=64"):
+        abi.call("gdn_prefill_noalloc_hip", *([FAKE] * 5), 0.0, FAKE, FAKE, None, 0.0, FAKE, FAKE,
+                 1, 16, 64, 64, 128, None)
+
+
 def test_decode_validation_errors():
     with pytest.raises(GdnError, match="UNSUPPORTED.*dk=64"):
         abi.call("gdn_decode_hip", *([FAKE] * 8), 0.1, FAKE, FAKE, 2, 2, 64, 128, None)
