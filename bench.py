@@ -2,28 +2,31 @@
 """Headline benchmark of the Gated DeltaNet hot paths on one MI355X.
 
 Metric (the brief's): prefill tokens/s at T=8192 + decode steps/s at B=256,
-with the achieved MFMA / HBM roofline fractions.
+with the achieved MFMA / HBM roofline fractions.  Every one of the brief's
+five configs gets a line in the same JSON object, each with its throughput,
+its roofline fraction, the CPU oracle (a restatement of the reference's
+PyTorch code, oracle/) timed on this host on the same inputs, and the
+same-run parity of the GPU results against that oracle:
 
-* Primary line (``value``): chunked prefill, B=1, T=8192, H=16, dk=dv=128,
+* primary line (``value``): chunked prefill, B=1, T=8192, H=16, dk=dv=128,
   chunk 64, zero initial state, seeded synthetic bf16 inputs already resident
-  in HBM.  One step = one ``prefill.prefill`` call (both kernels).
-* ``decode``: B=256, H=32, dk=dv=128, one 512 MiB fp32 state updated in place,
-  100 consecutive steps with fresh q/k/v/a/b per step (inputs pre-staged).
-* ``roofline``: the prefill state phase (the GEMM phase: map, scan and output
-  kernels, one ``gdn_prefill_state_hip`` call) against bf16 MFMA peak, with
-  the algorithmic state-recurrence FLOPs; ``decode.roofline``: the decode
-  kernel against HBM peak.  Durations come from HIP events around per-phase
-  launches on the stream the kernels run on.
-* ``cpu_baseline``: the CPU oracle (oracle/, a restatement of the reference's
-  PyTorch code) timed on this host on the same inputs, and the same-run parity
-  of the GPU results against it.
-* ``prefill_batches``: the same prefill at B=4 and B=8; ``prefill_varlen``:
-  config 3 (8 packed sequences, lengths U[512, 8192], nonzero initial
-  states); ``layer_e2e``: the end-to-end layer of config 5 (RMSNorm, fused
-  projection + conv + SiLU, prefill, output projection at B=4 x T=4096, then
-  decode steps at B=4).
+  in HBM.  One step = one ``prefill.prefill`` call (all kernels).
+  ``roofline``: the prefill's state phase (the GEMM phases: map, scan and
+  output kernels, one ``gdn_prefill_state_hip`` call) against bf16 MFMA
+  peak, with the algorithmic state-recurrence FLOPs; durations come from HIP
+  events around per-phase launches on the stream the kernels run on.
+* ``prefill_cfg2``: config 2, B=1, T=2048, H=16.
+* ``prefill_batches``: the metric prefill at B=4 and B=8 (timing only).
+* ``prefill_varlen``: config 4, 8 packed sequences, lengths U[512, 8192]
+  (seed 3), nonzero initial states.
+* ``decode``: config 3, B=256, H=32, dk=dv=128, one 512 MiB fp32 state
+  updated in place, 100 consecutive steps with fresh q/k/v/a/b per step.
+* ``layer_e2e``: config 5, the whole layer (RMSNorm, fused projection + conv
+  + SiLU, prefill, output projection) at B=4 x T=4096, then decode steps at
+  B=4 continuing from the prefill state.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-extra]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+                    [--no-extra] [--only prefill,cfg2,batches,varlen,decode,layer]
 """
 
 import argparse
@@ -37,13 +40,13 @@ import time
 # ---- algorithmic work (per unit), kept next to the formulas they come from ----
 C, K, V = 64, 128, 128
 PREFILL_FLOP_PER_TOKEN_HEAD = 2 * (3 * C * K + 2 * C * V + 3 * K * V)       # 180,224: whole path
-STATE_FLOP_PER_TOKEN_HEAD = 2 * (3 * K * V + 2 * C * V)                      # 131,072: state kernel
+STATE_FLOP_PER_TOKEN_HEAD = 2 * (3 * K * V + 2 * C * V)                      # 131,072: state kernels
 INTRA_FLOP_PER_TOKEN_HEAD = 2 * (2 * C * K)                                  # 32,768: intra kernel
 
 
-def prefill_bytes(B, T, H, has_state=False):
+def prefill_bytes(ntok, H, nseq, has_state=False):
     """Algorithmic HBM bytes of one prefill (bf16 q,k,v,o,a,b; fp32 mask, states)."""
-    return B * T * H * (2 * (2 * K + V) + 2 * V + 4) + 4 * B * T + 4 * B * H * K * V * (1 + int(has_state))
+    return ntok * H * (2 * (2 * K + V) + 2 * V + 4) + 4 * ntok + 4 * nseq * H * K * V * (1 + int(has_state))
 
 
 def decode_bytes(B, H):
@@ -53,6 +56,7 @@ def decode_bytes(B, H):
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+LEGS = ("prefill", "cfg2", "batches", "varlen", "decode", "layer")
 
 
 def measured_traffic(kernel):
@@ -92,6 +96,36 @@ def time_events(fn, iters, torch):
     return s.elapsed_time(e) / iters
 
 
+def time_cpu(fn, reps):
+    """Seconds per call of fn() after one warm-up call, and the warm-up's result."""
+    res = fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps, res
+
+
+def out_parity(out, ref, atol=2e-2, rtol=2e-2):
+    """The brief's bf16 bar: max |diff|, whether allclose(atol, rtol) holds, and the
+    error relative to the output's scale (max |diff| / max |ref|)."""
+    o, r = out.float().cpu(), ref.float().cpu()
+    d = (o - r).abs()
+    return {"max_abs_err": d.max().item(), "within_2e-2": bool((d <= atol + rtol * r.abs()).all()),
+            "max_err_over_max_ref": d.max().item() / max(r.abs().max().item(), 1e-30)}
+
+
+def rel_fro(x, ref):
+    x, ref = x.double().cpu(), ref.double().cpu()
+    return ((x - ref).norm() / ref.norm()).item()
+
+
+def roofline_fracs(flop, nbytes, ms):
+    """Achieved MFMA and HBM fractions of a timed call from its algorithmic work."""
+    tf = flop / (ms / 1e3) / 1e12
+    gbs = nbytes / (ms / 1e3) / 1e9
+    return {"tflops": tf, "mfma_frac": tf / PEAK_BF16_TFLOPS, "gbs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,9 +135,8 @@ def main():
     ap.add_argument("--T", type=int, default=8192)
     ap.add_argument("--B", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extra", action="store_true",
-                    help="skip the B=4/8 prefill lines, the packed varlen prefill (config 3) and the "
-                         "end-to-end layer (config 5) timing")
+    ap.add_argument("--no-extra", action="store_true", help="only the metric prefill and the config-3 decode")
+    ap.add_argument("--only", default="", help="comma list of legs to run: " + ",".join(LEGS))
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device copies of exactly 256 MiB (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -114,6 +147,15 @@ def main():
               "GDN hot path needs no collective (heads and sequences shard with no exchange); "
               "run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    legs = set(LEGS)
+    if args.no_extra:
+        legs = {"prefill", "decode"}
+    if args.only:
+        legs = {x.strip() for x in args.only.split(",") if x.strip()}
+        unknown = legs - set(LEGS)
+        if unknown:
+            ap.error(f"unknown legs {sorted(unknown)}")
+    cpu = not args.no_cpu_baseline
 
     import torch
     from gdn_18646_amd import abi, compile_kernels, synth
@@ -121,6 +163,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     exts = compile_kernels()
+    if cpu:
+        torch.set_num_threads(os.cpu_count() or 1)
+    nthr = torch.get_num_threads()
+    cpu_desc = f"{os.cpu_count()} logical CPUs ({cpu_model()})"
     if args.copy_calibration:
         src = torch.ones(64 << 20, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
@@ -128,74 +174,129 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    B, T, H = args.B, args.T, 16
-
-    # ------------------------------------------------------------------ prefill
-    d = synth.prefill_inputs(B, T, H, K, V, seed=1)
-    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    H = 16
     empty = torch.empty(0, device=dev, dtype=torch.float32)
     pf = exts["prefill"]
+    result = {}
 
-    def prefill_step():
-        return pf.prefill(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"], g["mask"], empty, 0.0)
+    def on_dev(d):
+        return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
 
-    for _ in range(args.warmup):
-        prefill_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ms_prefill = time_events(prefill_step, args.steps, torch)
-    wall_prefill = (time.perf_counter() - t0) / args.steps * 1e3
-    out_gpu, S_gpu = prefill_step()
-    torch.cuda.synchronize()
+    def prefill_call(g, state=None):
+        return pf.prefill(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"], g["mask"],
+                          empty if state is None else state, 0.0)
 
-    # per-phase kernel timing through the C ABI (same stream as torch's current one)
-    ws_bytes = abi.load().gdn_prefill_workspace_bytes(B, H, T, K, V)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    out_ph = torch.empty_like(out_gpu)
-    S_ph = torch.empty_like(S_gpu)
-    stream = torch.cuda.current_stream().cuda_stream
-    ptrs = (g["q"].data_ptr(), g["k"].data_ptr(), g["v"].data_ptr(), g["A_log"].data_ptr(), g["a"].data_ptr(),
-            0.0, g["b_logits"].data_ptr(), g["mask"].data_ptr(), None, 0.0, out_ph.data_ptr(), S_ph.data_ptr(),
-            B, H, T, K, V, ws.data_ptr(), ws_bytes, stream)
-    abi.call("gdn_prefill_hip", *ptrs)
-    ms_intra = time_events(lambda: abi.call("gdn_prefill_intra_hip", *ptrs), args.steps, torch)
-    ms_state = time_events(lambda: abi.call("gdn_prefill_state_hip", *ptrs), args.steps, torch)
+    def prefill_oracle(d, reps):
+        from oracle.prefill_ref import ref_prefill
+        dt_t = torch.tensor(0.0)
+        return time_cpu(lambda: ref_prefill(d["q"], d["k"], d["v"], d["A_log"], d["a"], dt_t, d["b_logits"],
+                                            d["mask"], state_in=None, scale=0.0, chunk_size=C), reps)
 
-    tokens = B * T
-    tok_s = tokens / (ms_prefill / 1e3)
-    state_tflops = STATE_FLOP_PER_TOKEN_HEAD * tokens * H / (ms_state / 1e3) / 1e12
-    intra_tflops = INTRA_FLOP_PER_TOKEN_HEAD * tokens * H / (ms_intra / 1e3) / 1e12
-    path_tflops = PREFILL_FLOP_PER_TOKEN_HEAD * tokens * H / (ms_prefill / 1e3) / 1e12
-    path_gbs = prefill_bytes(B, T, H) / (ms_prefill / 1e3) / 1e9
-    log(f"prefill B={B} T={T} H={H}: {ms_prefill:.4f} ms/step ({wall_prefill:.4f} ms wall), {tok_s:.4g} tok/s; "
-        f"intra {ms_intra:.4f} ms ({intra_tflops:.1f} TF/s), state {ms_state:.4f} ms ({state_tflops:.1f} TF/s); "
-        f"path {path_tflops:.1f} TF/s, {path_gbs:.0f} GB/s")
+    # ------------------------------------------------------------------ prefill (metric)
+    B, T = args.B, args.T
+    tok_s = ms_prefill = None
+    if "prefill" in legs:
+        d = synth.prefill_inputs(B, T, H, K, V, seed=1)
+        g = on_dev(d)
+        for _ in range(args.warmup):
+            prefill_call(g)
+        torch.cuda.synchronize()
+        ms_prefill = time_events(lambda: prefill_call(g), args.steps, torch)
+        out_gpu, S_gpu = prefill_call(g)
+        torch.cuda.synchronize()
+
+        # per-phase kernel timing through the C ABI (same stream as torch's current one)
+        ws_bytes = abi.load().gdn_prefill_workspace_bytes(B, H, T, K, V)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        out_ph = torch.empty_like(out_gpu)
+        S_ph = torch.empty_like(S_gpu)
+        stream = torch.cuda.current_stream().cuda_stream
+        ptrs = (g["q"].data_ptr(), g["k"].data_ptr(), g["v"].data_ptr(), g["A_log"].data_ptr(), g["a"].data_ptr(),
+                0.0, g["b_logits"].data_ptr(), g["mask"].data_ptr(), None, 0.0, out_ph.data_ptr(), S_ph.data_ptr(),
+                B, H, T, K, V, ws.data_ptr(), ws_bytes, stream)
+        abi.call("gdn_prefill_hip", *ptrs)
+        ms_intra = time_events(lambda: abi.call("gdn_prefill_intra_hip", *ptrs), args.steps, torch)
+        ms_state = time_events(lambda: abi.call("gdn_prefill_state_hip", *ptrs), args.steps, torch)
+        del ws, out_ph, S_ph
+
+        tokens = B * T
+        tok_s = tokens / (ms_prefill / 1e3)
+        state_tflops = STATE_FLOP_PER_TOKEN_HEAD * tokens * H / (ms_state / 1e3) / 1e12
+        intra_tflops = INTRA_FLOP_PER_TOKEN_HEAD * tokens * H / (ms_intra / 1e3) / 1e12
+        path = roofline_fracs(PREFILL_FLOP_PER_TOKEN_HEAD * tokens * H, prefill_bytes(tokens, H, B), ms_prefill)
+        log(f"prefill B={B} T={T} H={H}: {ms_prefill:.4f} ms/step, {tok_s:.4g} tok/s; intra {ms_intra:.4f} ms "
+            f"({intra_tflops:.1f} TF/s), state {ms_state:.4f} ms ({state_tflops:.1f} TF/s); "
+            f"path {path['tflops']:.1f} TF/s, {path['gbs']:.0f} GB/s")
+        result["roofline"] = {
+            "bound": "mfma",
+            "kernel": "gdn_prefill_state_hip (map + scan + output kernels)",
+            "achieved": state_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": state_tflops / PEAK_BF16_TFLOPS,
+            "traffic": measured_traffic("prefill_state") if (B, T) == (1, 8192) else None,
+            "flop_per_launch": STATE_FLOP_PER_TOKEN_HEAD * tokens * H, "kernel_ms": ms_state,
+        }
+        result["prefill_phases"] = {
+            "intra_ms": ms_intra, "intra_tflops": intra_tflops, "state_ms": ms_state, "state_tflops": state_tflops,
+            "path_tflops": path["tflops"], "path_mfma_frac": path["mfma_frac"],
+            "path_gbs": path["gbs"], "path_hbm_frac": path["hbm_frac"],
+            "path_flop": PREFILL_FLOP_PER_TOKEN_HEAD * tokens * H, "path_bytes": prefill_bytes(tokens, H, B),
+        }
+        if cpu:
+            sec, (o_ref, S_ref) = prefill_oracle(d, 3)
+            result["cpu_baseline"] = dict(
+                value=tokens / sec, unit="tokens/s", cores=nthr, kind="port",
+                sample=f"oracle.prefill_ref.ref_prefill (float32 torch CPU) on the same B={B} T={T} H={H} inputs, "
+                       f"1 warm-up + 3 timed calls, {sec * 1e3:.0f} ms/call; {cpu_desc}")
+            par = out_parity(out_gpu, o_ref)
+            result["parity"] = {"prefill_out_max_abs_err": par["max_abs_err"],
+                                "prefill_out_within_2e-2": par["within_2e-2"],
+                                "prefill_state_rel_fro": rel_fro(S_gpu, S_ref)}
+            log(f"  cpu oracle {sec * 1e3:.0f} ms/call ({nthr} threads); parity {result['parity']}")
+        del d, g, out_gpu, S_gpu
+
+    # ------------------------------------------------------------------ config 2: B=1, T=2048
+    if "cfg2" in legs:
+        d2 = synth.prefill_inputs(1, 2048, H, K, V, seed=1)
+        g2 = on_dev(d2)
+        for _ in range(3):
+            prefill_call(g2)
+        ms2 = time_events(lambda: prefill_call(g2), args.steps, torch)
+        o2, S2 = prefill_call(g2)
+        torch.cuda.synchronize()
+        leg = {"config": "config 2: B=1, T=2048, H=16, dk=dv=128, seed 1, zero initial state",
+               "ms": ms2, "tokens_per_s": 2048 / (ms2 / 1e3),
+               **roofline_fracs(PREFILL_FLOP_PER_TOKEN_HEAD * 2048 * H, prefill_bytes(2048, H, 1), ms2)}
+        if cpu:
+            sec, (o_ref, S_ref) = prefill_oracle(d2, 3)
+            leg["cpu_baseline"] = dict(value=2048 / sec, unit="tokens/s", cores=nthr, kind="port",
+                                       sample=f"oracle.prefill_ref.ref_prefill on the same inputs, 1 warm-up + 3 "
+                                              f"timed calls, {sec * 1e3:.0f} ms/call")
+            leg["parity"] = {**out_parity(o2, o_ref), "state_rel_fro": rel_fro(S2, S_ref)}
+        result["prefill_cfg2"] = leg
+        log(f"prefill cfg2 B=1 T=2048: {ms2:.4f} ms/step, {2048 / (ms2 / 1e3):.4g} tok/s, "
+            f"parity {leg.get('parity')}")
+        del d2, g2, o2, S2
 
     # ------------------------------------------------------------ prefill, B = 4 and 8
-    batches = {}
-    if not args.no_extra:
+    if "batches" in legs:
+        batches = {}
         for Bx in (4, 8):
-            dx = synth.prefill_inputs(Bx, T, H, K, V, seed=1)
-            gx = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in dx.items()}
-
-            def step_x():
-                return pf.prefill(gx["q"], gx["k"], gx["v"], gx["A_log"], gx["a"], 0.0, gx["b_logits"], gx["mask"],
-                                  empty, 0.0)
-
+            gx = on_dev(synth.prefill_inputs(Bx, T, H, K, V, seed=1))
             for _ in range(2):
-                step_x()
-            msx = time_events(step_x, max(3, args.steps // 2), torch)
+                prefill_call(gx)
+            msx = time_events(lambda: prefill_call(gx), max(3, args.steps // 2), torch)
             batches[f"B{Bx}"] = {"ms": msx, "tokens_per_s": Bx * T / (msx / 1e3),
-                                 "path_tflops": PREFILL_FLOP_PER_TOKEN_HEAD * Bx * T * H / (msx / 1e3) / 1e12}
+                                 **roofline_fracs(PREFILL_FLOP_PER_TOKEN_HEAD * Bx * T * H,
+                                                  prefill_bytes(Bx * T, H, Bx), msx)}
             log(f"prefill B={Bx} T={T} H={H}: {msx:.4f} ms/step, {Bx * T / (msx / 1e3):.4g} tok/s")
-            del dx, gx
+            del gx
+        result["prefill_batches"] = batches
 
-    # ------------------------------------- packed variable-length prefill (config 3)
-    varlen = None
-    if not args.no_extra:
+    # ------------------------------------- packed variable-length prefill (config 4)
+    if "varlen" in legs:
         lengths = synth.varlen_lengths(8, 512, 8192, seed=3)
         dl = synth.varlen_inputs(lengths, H, K, V, seed=3)
-        gl_ = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in dl.items()}
+        gl_ = on_dev(dl)
 
         def step_vl():  # offsets from the host, as a serving loop has them
             return pf.prefill_varlen(gl_["q"], gl_["k"], gl_["v"], gl_["A_log"], gl_["a"], 0.0, gl_["b_logits"],
@@ -204,59 +305,115 @@ def main():
         for _ in range(2):
             step_vl()
         msv = time_events(step_vl, max(3, args.steps // 2), torch)
+        ov, Sv = step_vl()
+        torch.cuda.synchronize()
         ntok = int(sum(lengths))
-        varlen = {"config": "8 packed sequences, lengths U[512, 8192] (seed 3): " + ",".join(map(str, lengths)) +
-                            f"; H={H}, dk=dv={K}, nonzero initial states",
-                  "tokens": ntok, "ms": msv, "tokens_per_s": ntok / (msv / 1e3),
-                  "path_tflops": PREFILL_FLOP_PER_TOKEN_HEAD * ntok * H / (msv / 1e3) / 1e12}
-        log(f"prefill varlen ({ntok} tokens in 8 sequences): {msv:.4f} ms/call, {ntok / (msv / 1e3):.4g} tok/s")
-        del dl, gl_
+        leg = {"config": "config 4: 8 packed sequences, lengths U[512, 8192] (seed 3): " + ",".join(map(str, lengths))
+                         + f"; H={H}, dk=dv={K}, nonzero initial states",
+               "tokens": ntok, "ms": msv, "tokens_per_s": ntok / (msv / 1e3),
+               **roofline_fracs(PREFILL_FLOP_PER_TOKEN_HEAD * ntok * H, prefill_bytes(ntok, H, 8, True), msv)}
+        if cpu:
+            from oracle.prefill_ref import ref_prefill_varlen
+            sec, (o_ref, S_ref) = time_cpu(
+                lambda: ref_prefill_varlen(dl["q"], dl["k"], dl["v"], dl["A_log"], dl["a"], 0.0, dl["b_logits"],
+                                           dl["cu_seqlens"], state_in=dl["state_in"], chunk_size=C), 1)
+            leg["cpu_baseline"] = dict(value=ntok / sec, unit="tokens/s", cores=nthr, kind="port",
+                                       sample=f"oracle.prefill_ref.ref_prefill_varlen on the same packed inputs, "
+                                              f"1 warm-up + 1 timed call, {sec * 1e3:.0f} ms/call")
+            leg["parity"] = {**out_parity(ov, o_ref),
+                             "state_rel_fro_max": max(rel_fro(Sv[i], S_ref[i]) for i in range(len(lengths)))}
+        result["prefill_varlen"] = leg
+        log(f"prefill varlen ({ntok} tokens in 8 sequences): {msv:.4f} ms/call, {ntok / (msv / 1e3):.4g} tok/s, "
+            f"parity {leg.get('parity')}")
+        del dl, gl_, ov, Sv
 
-    # ------------------------------------------------------------------ decode
-    DB, DH = 256, 32
-    dd = synth.decode_inputs(DB, DH, K, V, seed=2)
-    stream_in = synth.decode_step_stream(args.decode_steps, DB, DH, K, V, seed=2)
-    gsteps = [{k: v.to(dev) for k, v in st.items()} for st in stream_in]
-    A_log_d, dtb_d = dd["A_log"].to(dev), dd["dt_bias"].to(dev)
-    S_dev = dd["S"].to(dev)
-    o_dev = torch.empty(DB, DH, V, device=dev)
-    dec = exts["decode"]
-    scale = K ** -0.5
+    # ------------------------------------------------------------------ decode (config 3)
+    if "decode" in legs:
+        DB, DH = 256, 32
+        dd = synth.decode_inputs(DB, DH, K, V, seed=2)
+        stream_in = synth.decode_step_stream(args.decode_steps, DB, DH, K, V, seed=2)
+        gsteps = [{k: v.to(dev) for k, v in st.items()} for st in stream_in]
+        A_log_d, dtb_d = dd["A_log"].to(dev), dd["dt_bias"].to(dev)
+        S_dev = dd["S"].to(dev)
+        o_dev = torch.empty(DB, DH, V, device=dev)
+        dec = exts["decode"]
+        scale = K ** -0.5
 
-    # parity leg: 3 steps from S0 on a copy, checked against the oracle below
-    S_chk = S_dev.clone()
-    o_chk = []
-    for st in gsteps[:3]:
-        dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_chk, scale, o_dev, S_chk)
-        o_chk.append(o_dev.cpu())
-    S_chk = S_chk.cpu()
+        # parity leg: 3 steps from S0 on a copy, checked against the oracle below
+        S_chk = S_dev.clone()
+        o_chk = []
+        for st in gsteps[:3]:
+            dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_chk, scale, o_dev, S_chk)
+            o_chk.append(o_dev.cpu())
+        S_chk = S_chk.cpu()
 
-    for i in range(max(args.warmup, 1)):
-        st = gsteps[i % len(gsteps)]
-        dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_dev, scale, o_dev, S_dev)
-    it = iter(range(10 ** 9))
+        for i in range(max(args.warmup, 1)):
+            st = gsteps[i % len(gsteps)]
+            dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_dev, scale, o_dev, S_dev)
+        it = iter(range(10 ** 9))
 
-    def decode_step():
-        st = gsteps[next(it) % len(gsteps)]
-        dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_dev, scale, o_dev, S_dev)
+        def decode_step():
+            st = gsteps[next(it) % len(gsteps)]
+            dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_dev, scale, o_dev, S_dev)
 
-    ms_decode = time_events(decode_step, args.decode_steps, torch)
-    dec_gbs = decode_bytes(DB, DH) / (ms_decode / 1e3) / 1e9
-    log(f"decode B={DB} H={DH}: {ms_decode * 1e3:.1f} us/step, {1e3 / ms_decode:.1f} steps/s, {dec_gbs:.0f} GB/s")
+        ms_decode = time_events(decode_step, args.decode_steps, torch)
+        dec_gbs = decode_bytes(DB, DH) / (ms_decode / 1e3) / 1e9
+        log(f"decode B={DB} H={DH}: {ms_decode * 1e3:.1f} us/step, {1e3 / ms_decode:.1f} steps/s, {dec_gbs:.0f} GB/s")
+        leg = {
+            "value": 1e3 / ms_decode, "unit": "steps/s", "ms_per_step": ms_decode, "steps": args.decode_steps,
+            "config": {"workload": "config 3: GDN decode B=256 H=32 dk=dv=128, fp32 state in place, fresh q/k/v "
+                                   "each step", "B": DB, "H": DH, "dk": K, "dv": V},
+            "dtype": "fp32",
+            "roofline": {"bound": "hbm", "kernel": "gdn_decode_kernel", "achieved": dec_gbs, "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": dec_gbs / PEAK_HBM_GBS, "traffic": measured_traffic("decode"),
+                         "bytes_per_launch": decode_bytes(DB, DH), "kernel_ms": ms_decode},
+            "cpu_baseline": None,
+        }
+        if cpu:
+            from oracle.decode_ref import ref_decode
+            S_cpu = dd["S"]
+            o_refs = []
+
+            def cpu_dec(st, S):
+                return ref_decode(st["q"].reshape(DB, 1, DH, K), st["k"].reshape(DB, 1, DH, K),
+                                  st["v"].reshape(DB, 1, DH, V), S, dd["A_log"], st["a"].reshape(DB, 1, DH),
+                                  dd["dt_bias"], st["b"].reshape(DB, 1, DH), scale)
+
+            t0 = None
+            nd = 5
+            for i in range(nd + 1):  # step 0 is the warm-up
+                if i == 1:
+                    t0 = time.perf_counter()
+                o_r, S_cpu = cpu_dec(stream_in[i % len(stream_in)], S_cpu)
+                if i < 3:
+                    o_refs.append(o_r)
+                if i == 2:
+                    S_ref3 = S_cpu.clone()
+            cpu_dms = (time.perf_counter() - t0) / nd * 1e3
+            leg["cpu_baseline"] = dict(value=1e3 / cpu_dms, unit="steps/s", cores=nthr, kind="port",
+                                       sample=f"oracle.decode_ref.ref_decode on the same B={DB} H={DH} state and "
+                                              f"inputs, 1 warm-up + {nd} timed steps, {cpu_dms:.0f} ms/step")
+            leg["parity"] = {"out_max_abs_err": max((a - b).abs().max().item() for a, b in zip(o_chk, o_refs)),
+                             "state_rel_fro_3steps": rel_fro(S_chk, S_ref3)}
+            result.setdefault("parity", {}).update(
+                {"decode_out_max_abs_err": leg["parity"]["out_max_abs_err"],
+                 "decode_state_rel_fro_3steps": leg["parity"]["state_rel_fro_3steps"]})
+        result["decode"] = leg
+        del gsteps, S_dev, S_chk
 
     # ------------------------------------------------- end-to-end layer (config 5)
-    layer_e2e = None
-    if not args.no_extra:
+    if "layer" in legs:
         from gdn_18646_amd.gdn_layer import GDNLayerCustom, make_weights
 
+        LD, LH, LB, LT = 2048, 16, 4, 4096
         gl = torch.Generator().manual_seed(5)
-        wl = {k: v.to(dev) for k, v in make_weights(device="cpu", D=2048, H=16, DK=128, DV=128, std=0.02,
-                                                     generator=gl).items()}
+        w_cpu = make_weights(device="cpu", D=LD, H=LH, DK=128, DV=128, std=0.02, generator=gl)
+        wl = on_dev(w_cpu)
         layer = GDNLayerCustom(wl, exts)
-        LB, LT = 4, 4096
-        xl = torch.randn(LB, LT, 2048, generator=gl).bfloat16().to(dev)
-        xd = [torch.randn(LB, 1, 2048, generator=gl).bfloat16().to(dev) for _ in range(8)]
-        _, st_l = layer.forward(xl, return_state=True)
+        x_cpu = torch.randn(LB, LT, LD, generator=gl).bfloat16()
+        xl = x_cpu.to(dev)
+        xd = [torch.randn(LB, 1, LD, generator=gl).bfloat16().to(dev) for _ in range(8)]
+        y_l, st_l = layer.forward(xl, return_state=True)
         ms_lf = time_events(lambda: layer.forward(xl), max(3, args.steps // 4), torch)
         it_l = iter(range(10 ** 9))
 
@@ -275,72 +432,48 @@ def main():
         for _ in range(3):
             layer_dec_graph()
         ms_ldg = time_events(layer_dec_graph, 128, torch)
-        layer_e2e = {"config": "hidden 2048, H=16, dk=dv=128, conv 4, weights N(0, 0.02); prefill B=4 x T=4096, "
-                               "then decode steps at B=4 continuing from the prefill state",
-                     "prefill_ms": ms_lf, "prefill_tokens_per_s": LB * LT / (ms_lf / 1e3),
-                     "decode_ms_per_step": ms_ld, "decode_steps_per_s": 1e3 / ms_ld,
-                     "decode_graph_ms_per_step": ms_ldg, "decode_graph_steps_per_s": 1e3 / ms_ldg}
+        ncols = 2 * LH * 128 + LH * 128 + 2 * LH
+        lflop = (2 * LB * LT * LD * ncols + PREFILL_FLOP_PER_TOKEN_HEAD * LB * LT * LH + 2 * LB * LT * LH * 128 * LD)
+        lbytes = (2 * LB * LT * LD * 2 + 2 * ncols * LD + 2 * LD * LH * 128 +
+                  prefill_bytes(LB * LT, LH, LB) - 4 * LB * LT)  # x in, y out, weights, prefill (no mask)
+        dbytes = 2 * ncols * LD + 2 * LD * LH * 128 + LB * LH * 8 * 128 * 128 + 4 * LB * LD
+        leg = {"config": "config 5: hidden 2048, H=16, dk=dv=128, conv 4, weights N(0, 0.02); prefill B=4 x "
+                         "T=4096, then decode steps at B=4 continuing from the prefill state",
+               "prefill_ms": ms_lf, "prefill_tokens_per_s": LB * LT / (ms_lf / 1e3),
+               "prefill_roofline": {**roofline_fracs(lflop, lbytes, ms_lf), "flop": lflop, "bytes": lbytes},
+               "decode_ms_per_step": ms_ld, "decode_steps_per_s": 1e3 / ms_ld,
+               "decode_roofline": {**roofline_fracs(0, dbytes, ms_ld), "bytes": dbytes},
+               "decode_graph_ms_per_step": ms_ldg, "decode_graph_steps_per_s": 1e3 / ms_ldg}
         log(f"layer (config 5): prefill B={LB} T={LT} {ms_lf:.3f} ms ({LB * LT / (ms_lf / 1e3):.4g} tok/s), "
             f"decode B={LB} {ms_ld * 1e3:.1f} us/step eager, {ms_ldg * 1e3:.1f} us/step as a HIP graph")
-        del layer, wl, xl, st_l, step_g
+        del step_g
+        # decode == prefill at config 5: 32 decode steps from the prefill state of the
+        # first 4064 tokens against the forward over all 4096 (GPU against GPU)
+        _, st_full = layer.forward(xl, return_state=True)  # st_l was advanced by the timed decode steps
+        _, st_p = layer.forward(xl[:, :LT - 32], return_state=True)
+        ys = [layer.decode(xl[:, t:t + 1], st_p, inplace=True)[0] for t in range(LT - 32, LT)]
+        torch.cuda.synchronize()
+        yd = torch.cat(ys, 1)
+        leg["parity"] = {"decode32_vs_prefill": out_parity(yd, y_l[:, LT - 32:]),
+                         "decode32_state_rel_fro": rel_fro(st_p["recurrent"], st_full["recurrent"])}
+        if cpu:
+            from oracle.layer_ref import GDNLayerBaseline
+            y0 = y_l[:1].cpu()
+            t0 = time.perf_counter()
+            GDNLayerBaseline(w_cpu, chunk_size=C).forward(x_cpu[:1])
+            sec = time.perf_counter() - t0
+            y_ref = GDNLayerBaseline(w_cpu, chunk_size=C, fp32_proj=True).forward(x_cpu[:1])
+            leg["cpu_baseline"] = dict(value=LT / sec, unit="tokens/s", cores=nthr, kind="port",
+                                       sample="oracle.layer_ref.GDNLayerBaseline.forward (ref_rmsnorm, "
+                                              "ref_proj_conv_silu, ref_prefill, W_o) on sequence 0 of the same "
+                                              f"input (1 x 4096 tokens), one call, {sec:.2f} s")
+            leg["parity"]["forward_seq0_vs_oracle_fp32_proj"] = {**out_parity(y0, y_ref),
+                                                                 "rel_fro": rel_fro(y0, y_ref)}
+        result["layer_e2e"] = leg
+        log(f"  layer parity {leg['parity']}")
+        del layer, wl, xl, st_l
 
-    # ------------------------------------------------------------------ CPU oracle
-    cpu_prefill = cpu_decode = None
-    parity = {}
-    if not args.no_cpu_baseline:
-        from oracle.decode_ref import ref_decode
-        from oracle.prefill_ref import ref_prefill
-
-        torch.set_num_threads(os.cpu_count() or 1)
-        nthr = torch.get_num_threads()
-        dt_t = torch.tensor(0.0)
-
-        def cpu_pf():
-            return ref_prefill(d["q"], d["k"], d["v"], d["A_log"], d["a"], dt_t, d["b_logits"], d["mask"],
-                               state_in=None, scale=0.0, chunk_size=C)
-
-        o_ref, S_ref = cpu_pf()  # warm-up, also the parity reference
-        reps = 3
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            cpu_pf()
-        cpu_ms = (time.perf_counter() - t0) / reps * 1e3
-        cpu_prefill = dict(value=tokens / (cpu_ms / 1e3), unit="tokens/s", cores=nthr, kind="port",
-                           sample=f"oracle.prefill_ref.ref_prefill (float32 torch CPU) on the same B={B} T={T} "
-                                  f"H={H} inputs, 1 warm-up + {reps} timed calls, {cpu_ms:.0f} ms/call; "
-                                  f"{os.cpu_count()} logical CPUs ({cpu_model()})")
-        od = (out_gpu.float().cpu() - o_ref).abs()
-        parity["prefill_out_max_abs_err"] = od.max().item()
-        parity["prefill_out_within_2e-2"] = bool((od <= 2e-2 + 2e-2 * o_ref.abs()).all())
-        parity["prefill_state_rel_fro"] = ((S_gpu.cpu() - S_ref).norm() / S_ref.norm()).item()
-
-        S_cpu = dd["S"]
-        o_refs = []
-
-        def cpu_dec(st, S):
-            return ref_decode(st["q"].reshape(DB, 1, DH, K), st["k"].reshape(DB, 1, DH, K),
-                              st["v"].reshape(DB, 1, DH, V), S, dd["A_log"], st["a"].reshape(DB, 1, DH),
-                              dd["dt_bias"], st["b"].reshape(DB, 1, DH), scale)
-
-        t0 = None
-        nd = 5
-        for i in range(nd + 1):  # step 0 is the warm-up
-            if i == 1:
-                t0 = time.perf_counter()
-            o_r, S_cpu = cpu_dec(stream_in[i % len(stream_in)], S_cpu)
-            if i < 3:
-                o_refs.append(o_r)
-            if i == 2:
-                S_ref3 = S_cpu.clone()
-        cpu_dms = (time.perf_counter() - t0) / nd * 1e3
-        cpu_decode = dict(value=1e3 / cpu_dms, unit="steps/s", cores=nthr, kind="port",
-                          sample=f"oracle.decode_ref.ref_decode on the same B={DB} H={DH} state and inputs, "
-                                 f"1 warm-up + {nd} timed steps, {cpu_dms:.0f} ms/step")
-        parity["decode_out_max_abs_err"] = max((a - b).abs().max().item() for a, b in zip(o_chk, o_refs))
-        parity["decode_state_rel_fro_3steps"] = ((S_chk - S_ref3).norm() / S_ref3.norm()).item()
-        log(f"cpu oracle: prefill {cpu_ms:.0f} ms/call, decode {cpu_dms:.0f} ms/step, {nthr} threads; parity {parity}")
-
-    result = {
+    line = {
         "metric": "prefill tokens/s (T=8192) + decode steps/s (B=256); % of MFMA / HBM roofline",
         "value": tok_s,
         "unit": "tokens/s",
@@ -355,42 +488,9 @@ def main():
         "data": "synthetic (seeded: q,k unit-norm N(0,1), v,a,b N(0,1), A_log=ln0.5, dt_bias=0)",
         "config": {"workload": f"GDN chunked prefill B={B} T={T} H={H} dk=dv=128 chunk=64, zero initial state",
                    "B": B, "T": T, "H": H, "dk": K, "dv": V, "chunk": C},
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "gdn_prefill_state_hip (map + scan + output kernels)",
-            "achieved": state_tflops,
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": state_tflops / PEAK_BF16_TFLOPS,
-            "traffic": measured_traffic("prefill_state") if (B, T) == (1, 8192) else None,
-            "flop_per_launch": STATE_FLOP_PER_TOKEN_HEAD * tokens * H,
-            "kernel_ms": ms_state,
-        },
-        "prefill_phases": {
-            "intra_ms": ms_intra, "intra_tflops": intra_tflops,
-            "state_ms": ms_state, "state_tflops": state_tflops,
-            "path_tflops": path_tflops, "path_mfma_frac": path_tflops / PEAK_BF16_TFLOPS,
-            "path_gbs": path_gbs, "path_hbm_frac": path_gbs / PEAK_HBM_GBS,
-            "path_flop": PREFILL_FLOP_PER_TOKEN_HEAD * tokens * H, "path_bytes": prefill_bytes(B, T, H),
-        },
-        "prefill_batches": batches or None,
-        "prefill_varlen": varlen,
-        "layer_e2e": layer_e2e,
-        "decode": {
-            "value": 1e3 / ms_decode, "unit": "steps/s", "ms_per_step": ms_decode, "steps": args.decode_steps,
-            "config": {"workload": "GDN decode B=256 H=32 dk=dv=128, fp32 state in place, fresh q/k/v each step",
-                       "B": DB, "H": DH, "dk": K, "dv": V},
-            "dtype": "fp32",
-            "roofline": {"bound": "hbm", "kernel": "gdn_decode_kernel", "achieved": dec_gbs, "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": dec_gbs / PEAK_HBM_GBS,
-                         "traffic": measured_traffic("decode"),
-                         "bytes_per_launch": decode_bytes(DB, DH), "kernel_ms": ms_decode},
-            "cpu_baseline": cpu_decode,
-        },
-        "cpu_baseline": cpu_prefill,
-        "parity": parity or None,
     }
-    print(json.dumps(result), flush=True)
+    line.update(result)
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

@@ -49,6 +49,14 @@ using namespace gdn;
 constexpr int kC = 64;    // chunk length
 constexpr int kDK = 128;  // key / query dim
 
+// Workspace record of one (chunk, head), written by the intra kernel and read
+// by the state kernels, in 1 KiB MFMA fragments (lane l's 16 bytes at 16 l):
+// the six nonzero fragments of Tp, the six of Aq, then the gate block.
+constexpr int kRecTp = 0;
+constexpr int kRecAq = 6;
+constexpr int kRecG = 12;
+constexpr int kRecFrags = 13;
+
 struct PrefillParams {
     const uint16_t* q;
     const uint16_t* k;
@@ -61,9 +69,7 @@ struct PrefillParams {
     uint16_t* out;
     float* state_out;
     const int32_t* cu;  // varlen offsets (nullable: batch mode)
-    u32x4* wsT;
-    u32x4* wsA;
-    float* wsG;
+    u32x4* wsR;          // per (chunk, head) workspace records (kRecFrags 1 KiB fragments each)
     float dt_bias;
     float scale;
     int H;
@@ -118,6 +124,8 @@ __device__ __forceinline__ HeadItem head_major_xcd(int L, int per_head) {
 // The nonzero fragments (mt, s) of the causal Aq, in workspace order:
 // (0,0),(1,0),(2,0),(2,1),(3,0),(3,1) as f = 2 mt + s.
 __device__ __forceinline__ constexpr int aq_slot(int i) { return i < 2 ? 2 * i : i + 2; }
+// Inverse: slot of the nonzero fragment (mt, s) (s = 1 needs mt >= 2).
+__device__ __forceinline__ constexpr int aq_index(int mt, int s) { return mt < 2 ? mt : 2 * mt - 2 + s; }
 
 // ---------------------------------------------------------------------------
 // Kernel 1
@@ -205,6 +213,19 @@ __device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUn
         const int idx = tid + 256 * it, row = idx >> 4, c8 = (idx & 15) * 8;
         L.kv[it] = u32x4{0u, 0u, 0u, 0u};
         if (row < U.nvalid) L.kv[it] = *reinterpret_cast<const u32x4*>(p.k + (U.row_base + row) * kDK + c8);
+    }
+}
+
+// Tp fragments (mt, s) = (wave, 0), (wave, 1) of one record: fragments
+// (0, 1) and (1, 1) lie above the diagonal and are not stored; the others go
+// to slots (0,0) (1,0) (2,0) (2,1) (3,0) (3,1) in that order.
+__device__ __forceinline__ void store_tp(const PrefillParams& p, size_t wc, int wave, int lane, const u32x4 (&tpf)[2]) {
+    u32x4* rec = p.wsR + (wc * kRecFrags + kRecTp) * 64;
+    if (wave < 2) {
+        rec[wave * 64 + lane] = tpf[0];
+    } else {
+        rec[(2 * wave - 2) * 64 + lane] = tpf[0];
+        rec[(2 * wave - 1) * 64 + lane] = tpf[1];
     }
 }
 
@@ -342,15 +363,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     // then this unit's stores.
     if (N.valid) intra_load(p, N, tid, L);
     if (wave == 0) {
-        float* G = p.wsG + wc * 256;
+        float* G = reinterpret_cast<float*>(p.wsR + (wc * kRecFrags + kRecG) * 64);
         G[lane] = G0;
         G[64 + lane] = G1;
         G[128 + lane] = G2;
     }
-    if (have_prev) {
-        p.wsT[(wc_prev * 8 + 2 * wave) * 64 + lane] = tpf[0];
-        p.wsT[(wc_prev * 8 + 2 * wave + 1) * 64 + lane] = tpf[1];
-    }
+    if (have_prev) store_tp(p, wc_prev, wave, lane, tpf);
 
     // 4) The six nonzero Aq fragments (mt, s) = (0,0),(1,0),(2,0),(2,1),(3,0),(3,1):
     //    lane holds Aq[16mt + m][32s + pi(g, j)].
@@ -361,7 +379,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];
         const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
-        p.wsA[(wc * 6 + i) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        p.wsR[(wc * kRecFrags + kRecAq + i) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
 
     // 5) T = (I + A)^-1 in fp32, blocked by 16 (block rows / columns I, J),
@@ -508,10 +526,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     u = u_next;
     U = N;
     }
-    if (have_prev) {
-        p.wsT[(wc_prev * 8 + 2 * wave) * 64 + lane] = tpf[0];
-        p.wsT[(wc_prev * 8 + 2 * wave + 1) * 64 + lane] = tpf[1];
-    }
+    if (have_prev) store_tp(p, wc_prev, wave, lane, tpf);
 }
 
 // ---------------------------------------------------------------------------
@@ -530,8 +545,8 @@ struct Stage {
     static constexpr bool out = MODE == kModeOut;
     static constexpr int offK = 0;                                  // 16: (mt, s), lane slots swizzled (kslot)
     static constexpr int offQ = offK + 16 * kFragB;                 // 16 (out only)
-    static constexpr int offT = offQ + (out ? 16 : 0) * kFragB;     // 8: Tp (mt, s)
-    static constexpr int offA = offT + 8 * kFragB;                  // 6 (out only): Aq slots used
+    static constexpr int offT = offQ + (out ? 16 : 0) * kFragB;     // 6: nonzero Tp fragments
+    static constexpr int offA = offT + 6 * kFragB;                  // 6 (out only): Aq slots used
     static constexpr int offG = offA + (out ? 6 : 0) * kFragB;      // gamma, m scale gamma, gamma_C/gamma
     static constexpr int offV = offG + kFragB;
     static constexpr int vWave = 2 * NT * kFragB;
@@ -569,7 +584,7 @@ __device__ __forceinline__ int kslot_row(int slot) { return (slot & 15) ^ (4 * (
 template <int MODE, int NW, int NT>
 struct Stager {
     using St = Stage<MODE, NW, NT>;
-    static constexpr int nK = 16, nQ = St::out ? 16 : 0, nT = 8, nA = St::out ? 6 : 0;
+    static constexpr int nK = 16, nQ = St::out ? 16 : 0, nT = 6, nA = St::out ? 6 : 0;
     static constexpr int NJ = nK + nQ + nT + nA + 1;  // + the gate block
     const PrefillParams* p;
     lds_u8* buf;
@@ -602,14 +617,11 @@ struct Stager {
                     const int row = min(16 * (ff >> 2) + (isq ? m : kslot_row(lane)), nvalid - 1);
                     dma16(base, static_cast<uint32_t>((row * kDK + 32 * (ff & 3) + 8 * g) * 2), dst);
                 }
-            } else if (f < nK + nQ + nT) {
-                dma16(reinterpret_cast<const unsigned char*>(p->wsT + wc * 8 * 64) + (f - nK - nQ) * kFragB, L->fr,
-                      dst);
-            } else if (f < nK + nQ + nT + nA) {
-                dma16(reinterpret_cast<const unsigned char*>(p->wsA + wc * 6 * 64) + (f - nK - nQ - nT) * kFragB,
-                      L->fr, dst);
             } else {
-                dma16(p->wsG + wc * 256, L->fr, dst);
+                // record fragments: Tp, then Aq (output only), then the gate block
+                const unsigned char* rec = reinterpret_cast<const unsigned char*>(p->wsR + wc * kRecFrags * 64);
+                const int j = f - nK - nQ;
+                dma16(rec + (j < nT + nA ? j : kRecG) * kFragB, L->fr, dst);
             }
         }
         if (v_on) {
@@ -744,7 +756,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
                 }
         }
     }
-    bf16x8 tf[8], af[St::out ? 6 : 1], ktf[8][2];
+    bf16x8 tf[6], af[St::out ? 6 : 1], ktf[8][2];
     // With one wave per SIMD (NW <= 4) the Kt fragments are read here, while
     // (a) drains; with two (NW = 8) the other wave covers their latency, so
     // they are read just before (e) to keep this wave within 256 registers.
@@ -757,7 +769,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
         }
     };
 #pragma unroll
-    for (int f = 0; f < 8; ++f) tf[f] = frag(buf, St::offT + f * kFragB, lane);
+    for (int f = 0; f < 6; ++f) tf[f] = frag(buf, St::offT + f * kFragB, lane);
     if constexpr (kEarlyKt) load_kt();
     // V in the accumulator layout (column n, rows 16 mt + 4 g + i): one
     // transposing read per (mt, nt) -- source lane 4 j + a of group g reads
@@ -789,15 +801,16 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Tp is lower triangular: fragments (0, 1) and (1, 1) are zero and absent.
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         bf16x8 BY[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) BY[nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 2 * s; mt < 4; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) D[mt][nt] = mfma16x16x32(tf[2 * mt + s], BY[nt], D[mt][nt]);
+            for (int nt = 0; nt < NT; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[nt], D[mt][nt]);
     }
     if constexpr (St::out) {
 #pragma unroll
@@ -1089,6 +1102,423 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
     }
 }
 
+// ---------------------------------------------------------------------------
+// Kernel 2b: the state pass for dv % 128 == 0 -- four waves of 32 columns
+// ---------------------------------------------------------------------------
+// A workgroup owns 128 state columns of one (sequence, head, chunk group);
+// wave w owns columns 32 w .. 32 w + 31 as two 16-column MFMA tiles, so every
+// operand fragment it reads from LDS feeds two MFMAs.  (With 16-column waves,
+// eight per CU, the LDS reads of a chunk step outlast its MFMAs.)  The output
+// pass runs one workgroup per CU, one wave per SIMD with the whole register
+// file; the map pass two workgroups per CU.
+// Per chunk, DMA-staged into one of two LDS buffers:
+//   K   16 fragments, lane slots swizzled (kslot) for the K^T transposing reads
+//   Q   16 fragments (output pass)
+//   record: Tp 6, Aq 6 (output pass), gate block 1
+//   V   wave w's [64 rows][32 columns] bf16 at offV + 4 KiB w (not for phi columns)
+// Wave w copies a fixed share: K and Q fragments 4 w .. 4 w + 3 (row block w),
+// record fragments w, w + 4, w + 8, w + 12, and its own V columns.  Full chunks
+// take a path without per-row checks; a sequence's partial last chunk clamps
+// its copies to the sequence and predicates its output stores.  Rows past the
+// sequence end stay finite copies of the last row, and their Tp rows and
+// columns are zero (beta m = 0 there), so they add exact zeros.
+template <int MODE>
+struct Stage4 {
+    static constexpr bool out = MODE == kModeOut;
+    static constexpr int offK = 0;
+    static constexpr int offQ = 16 * kFragB;
+    static constexpr int offR = offQ + (out ? 16 : 0) * kFragB;
+    static constexpr int nRec = out ? kRecFrags : 7;  // the map pass copies Tp and the gate block
+    static constexpr int offTp = offR;
+    static constexpr int offAq = offR + kRecAq * kFragB;
+    static constexpr int offG = offR + (out ? kRecG : 6) * kFragB;
+    static constexpr int offV = offR + nRec * kFragB;
+    static constexpr int bytes = offV + 16 * kFragB;
+    static constexpr int stores = out ? 8 : 0;  // output stores per chunk per wave
+};
+
+// Per-lane byte offsets of the copies (fixed for the kernel).
+struct Lane4 {
+    uint32_t k, q, r, v;
+};
+
+// Issue chunk `c`'s copies of this wave into `buf`.  `row0`: q/k/v row of the
+// chunk's first token; `rec`: the chunk's record; `vcol0`: this wave's first
+// V column.
+template <int MODE, bool FULL>
+__device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf, size_t row0, const u32x4* rec,
+                                             int vcol0, int nvalid, int wave, int lane, const Lane4& L, bool v_on) {
+    using St = Stage4<MODE>;
+    // Full chunks: base at this wave's row block, fixed lane offsets.  The
+    // partial chunk: base at the chunk's first row and each lane's row
+    // clamped to the sequence, so every offset is non-negative and in range.
+    const unsigned char* kc = reinterpret_cast<const unsigned char*>(p.k + row0 * kDK);
+    const unsigned char* qc = reinterpret_cast<const unsigned char*>(p.q + row0 * kDK);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        lds_u8* kd = buf + St::offK + (4 * wave + s) * kFragB;
+        if (FULL) {
+            dma16(kc + 16 * wave * kDK * 2 + 64 * s, L.k, kd);
+        } else {
+            const int row = min(16 * wave + kslot_row(lane), nvalid - 1);
+            dma16(kc, static_cast<uint32_t>((row * kDK + 32 * s + 8 * (lane >> 4)) * 2), kd);
+        }
+    }
+    if constexpr (St::out) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            lds_u8* qd = buf + St::offQ + (4 * wave + s) * kFragB;
+            if (FULL) {
+                dma16(qc + 16 * wave * kDK * 2 + 64 * s, L.q, qd);
+            } else {
+                const int row = min(16 * wave + (lane & 15), nvalid - 1);
+                dma16(qc, static_cast<uint32_t>((row * kDK + 32 * s + 8 * (lane >> 4)) * 2), qd);
+            }
+        }
+    }
+    const unsigned char* rb = reinterpret_cast<const unsigned char*>(rec);
+#pragma unroll
+    for (int j0 = 0; j0 < St::nRec; j0 += 4) {
+        const int j = j0 + wave;
+        if (j < St::nRec) {
+            const int src = St::out ? j : (j < 6 ? j : kRecG);
+            dma16(rb + src * kFragB, L.r, buf + St::offR + j * kFragB);
+        }
+    }
+    if (v_on) {
+        const unsigned char* vb = reinterpret_cast<const unsigned char*>(p.v + row0 * p.dv + vcol0);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            lds_u8* vd = buf + St::offV + wave * 4 * kFragB + it * kFragB;
+            if (FULL) {
+                dma16(vb + static_cast<size_t>(16 * it) * p.dv * 2, L.v, vd);
+            } else {
+                const int row = min(16 * it + (lane >> 2), nvalid - 1);
+                dma16(vb, static_cast<uint32_t>((row * p.dv + 8 * (lane & 3)) * 2), vd);
+            }
+        }
+    }
+}
+
+// One chunk of the state recurrence for this wave's 128 x 32 state tile, the
+// chunk's operands staged in `buf`.  `ob`: out row of the chunk's first
+// token at this wave's first column (uniform).
+template <int MODE, bool FULL>
+__device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2], uint16_t* ob, int orow, int nvalid,
+                                            int wave, int lane, bool v_zero, uint32_t kt_lane) {
+    using St = Stage4<MODE>;
+    constexpr bool OUT = St::out;
+    const int n = lane & 15, g = lane >> 4;
+    const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + St::offG);
+    const lds_u8* Vs = buf + St::offV + wave * 4 * kFragB;
+
+    // (a) X = K S and P^T = S^T Q^T.  The state's bf16 copy is the B operand
+    //     of K S and the A operand of S^T Q^T as it stands (k = state rows
+    //     32 s + 8 g + j in both).
+    // The map pass runs two waves per SIMD within 256 registers: phase fences
+    // (PHASE()) keep the scheduler from hoisting every fragment read of the
+    // step to its top; the other wave covers the latency.  The output pass
+    // (one wave per SIMD, 512 registers) lets the reads run ahead.
+#define PHASE()                                        \
+    do {                                               \
+        if constexpr (!OUT) __builtin_amdgcn_sched_barrier(0); \
+    } while (0)
+    const float gC = G[kC - 1];
+    f32x4 X[4][2], P[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // In two k-halves, so the map pass holds half of the K fragments at a time.
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        bf16x8 kf[4][2], qf[OUT ? 4 : 1][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int f = 4 * mt + 2 * half + s2;
+                kf[mt][s2] = kfrag(buf + St::offK, f, lane);
+                if constexpr (OUT) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
+            }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int s = 2 * half + s2;
+            bf16x8 Bs[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    X[mt][nt] = mfma16x16x32(kf[mt][s2], Bs[nt], X[mt][nt]);
+                    if constexpr (OUT) P[mt][nt] = mfma16x16x32(Bs[nt], qf[mt][s2], P[mt][nt]);
+                }
+        }
+        PHASE();
+    }
+    // (b) Y = V - gamma o X (in place in X).  V in the accumulator layout
+    //     (column n, rows 16 mt + 4 g + i): source lane 4 j + a of group g of
+    //     a transposing read fetches row 16 mt + 4 g + j, columns 16 nt + 4 a ..
+    i16x4 vv[2][4];
+    const lds_u8* vrow = Vs + ((4 * g + ((lane >> 2) & 3)) * 32 + 4 * (lane & 3)) * 2;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            vv[nt][mt] = v_zero ? i16x4{0, 0, 0, 0}
+                                : __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vrow + (16 * mt * 32 + 16 * nt) * 2));
+    f32x4 gam[4], kd[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
+        kd[mt] = *reinterpret_cast<const lds_f32x4*>(G + 128 + 16 * mt + 4 * g);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                X[mt][nt][i] = bf2f(static_cast<uint16_t>(vv[nt][mt][i])) - gam[mt][i] * X[mt][nt][i];
+    // (c) dV = Tp Y (Tp lower triangular: six nonzero fragments).
+    bf16x8 tf[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) tf[i] = frag(buf, St::offTp + i * kFragB, lane);
+    f32x4 D[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        bf16x8 BY[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) BY[nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
+#pragma unroll
+        for (int mt = 2 * s; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[nt], D[mt][nt]);
+    }
+    PHASE();
+    // (d) S <- gamma_C S + K^T ((gamma_C / gamma) o dV).
+    bf16x8 ktf[8][2];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        ktf[r][0] = ktfrag(buf + St::offK, kt_lane, r, 0);
+        ktf[r][1] = ktfrag(buf + St::offK, kt_lane, r, 1);
+    }
+    bf16x8 BS0[2], BS1[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        BS0[nt] = pack8(kd[0] * D[0][nt], kd[1] * D[1][nt]);
+        BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            S[r][nt] *= gC;
+            S[r][nt] = mfma16x16x32(ktf[r][0], BS0[nt], S[r][nt]);
+            S[r][nt] = mfma16x16x32(ktf[r][1], BS1[nt], S[r][nt]);
+        }
+    // (e) O^T = (m scale gamma) o P^T + dV^T Aq^T: each lane holds 4
+    //     consecutive output columns of token 16 mt + n, stored as 8 bytes.
+    if constexpr (OUT) {
+        bf16x8 af[6];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offAq + i * kFragB, lane);
+        float co[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) co[mt] = G[64 + 16 * mt + n];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const bf16x8 BD0 = pack8(D[0][nt], D[1][nt]), BD1 = pack8(D[2][nt], D[3][nt]);
+            f32x4 O[4];
+            O[0] = mfma16x16x32(BD0, af[0], co[0] * P[0][nt]);
+            O[1] = mfma16x16x32(BD0, af[1], co[1] * P[1][nt]);
+            O[2] = mfma16x16x32(BD1, af[3], mfma16x16x32(BD0, af[2], co[2] * P[2][nt]));
+            O[3] = mfma16x16x32(BD1, af[5], mfma16x16x32(BD0, af[4], co[3] * P[3][nt]));
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int row = 16 * mt + n;
+                if (FULL || row < nvalid)
+                    *reinterpret_cast<u32x2*>(ob + row * orow + 16 * nt + 4 * g) = pack4_bf16(O[mt]);
+            }
+        }
+    }
+#undef PHASE
+}
+
+// The state pass of one workgroup: 128 columns of one (sequence, head,
+// chunk group) in the roles of gdn_prefill_state_kernel (output pass: from
+// the group's initial state, outputs and the final state; map pass: psi
+// columns from zero with V, phi columns from the identity without V).
+template <int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == kModeOut ? 1 : 2,
+                                                                      MODE == kModeOut ? 1 : 2))) void
+gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
+    using St = Stage4<MODE>;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][St::bytes];
+    lds_u8* const buf0 = (lds_u8*)&smem[0][0];
+    lds_u8* const buf1 = (lds_u8*)&smem[1][0];
+
+    const int wg = blockIdx.x;
+    int head, grp, vg, ngroups;
+    if (sg.plan) {
+        vg = wg % sg.nvg;
+        const int hh = (wg / sg.nvg) / sg.ngroups_run, q = (wg / sg.nvg) % sg.ngroups_run;
+        if (hh >= p.H || q >= sg.plan[MODE == kModeMap ? 1 : 0]) return;  // uniform over the workgroup
+        const int e = sg.plan[2 + 2 * sg.nseq + (MODE == kModeMap ? kPlanCap : 0) + q];
+        head = (e >> 8) * p.H + hh;
+        grp = e & 255;
+        ngroups = plan_groups(sg, e >> 8);
+    } else {
+        if (p.xcd_heads) {
+            const HeadItem hi = head_major_xcd(wg, sg.ngroups_run * sg.nvg);
+            head = hi.head;
+            grp = hi.item / sg.nvg;
+            vg = hi.item % sg.nvg;
+        } else {
+            vg = wg % sg.nvg;
+            head = (wg / sg.nvg) / sg.ngroups_run;
+            grp = (wg / sg.nvg) % sg.ngroups_run;
+        }
+        if (head * sg.ngroups_run + grp >= sg.nheads * sg.ngroups_run) return;  // uniform over the workgroup
+        ngroups = sg.ngroups;
+    }
+    const int sidx = head / p.H;
+    const int h = head % p.H;
+    const SeqInfo sq = seq_info(p, sidx);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15, g = lane >> 4;
+    const int dv = p.dv;
+    const int col0_wave = vg * 128 + 32 * wave;  // map pass: >= dv means identity columns
+    const bool phi_cols = MODE == kModeMap && vg * 128 >= dv;
+    const int vcol0 = phi_cols ? 0 : col0_wave;
+    const int nchunks = (sq.len + kC - 1) / kC;
+    const int glen = (nchunks + ngroups - 1) / ngroups;
+    const int c_begin = min(grp * glen, nchunks), c_end = min(c_begin + glen, nchunks);
+    const Lane4 L = {static_cast<uint32_t>(kslot_row(lane) * kDK * 2 + (lane >> 4) * 16),
+                     static_cast<uint32_t>((lane & 15) * kDK * 2 + (lane >> 4) * 16), static_cast<uint32_t>(16 * lane),
+                     static_cast<uint32_t>((lane >> 2) * dv * 2 + (lane & 3) * 16)};
+    const uint32_t kt_lane = kt_lane_offset(lane);
+
+    // State tile: S[r][nt][i] = S[rho(r, g, i)][col0_wave + 16 nt + n].
+    f32x4 S[8][2];
+    if constexpr (MODE == kModeMap) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    S[r][nt][i] = (phi_cols && rho_row(r, g, i) == col0_wave - dv + 16 * nt + n) ? 1.f : 0.f;
+    } else if (grp > 0) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const f32x4* Ps = reinterpret_cast<const f32x4*>(
+                sg.psi + (group_unit(sg, p.H, sidx, h, grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) S[r][nt] = Ps[r * 64 + lane];
+        }
+    } else if (p.state_in) {
+        const float* sin = p.state_in + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) S[r][nt][i] = sin[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
+    const int orow = p.out_tm ? p.H * dv : dv;
+    auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
+    auto obase = [&](int c) {
+        const size_t tok = static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + static_cast<size_t>(c) * kC;
+        return (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + col0_wave;
+    };
+    auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
+    auto rec = [&](int c) { return p.wsR + (static_cast<size_t>(sq.slot0 + c) * p.H + h) * kRecFrags * 64; };
+    auto issue = [&](int c, lds_u8* buf) {
+        // Opaque per call: otherwise the copies' LDS addresses (buffer, wave
+        // and fragment constants) are hoisted out of the chunk loop and held
+        // in SGPRs, which runs the output pass out of them.
+        int w = wave;
+        asm volatile("" : "+s"(w));
+        if (nval(c) == kC)
+            stage4_issue<MODE, true>(p, buf, rows(c), rec(c), vcol0, kC, w, lane, L, !phi_cols);
+        else
+            stage4_issue<MODE, false>(p, buf, rows(c), rec(c), vcol0, nval(c), w, lane, L, !phi_cols);
+    };
+    auto step = [&](int c, lds_u8* cur, lds_u8* nxt) {
+        // Chunk c's copies went out before chunk c-1's output stores (the
+        // one partial chunk of a sequence is always its group's last).
+        if (c == c_begin)
+            wait_vm<0>();
+        else
+            wait_vm<St::stores>();
+        lds_barrier();  // chunk c staged by every wave; nobody still reads `nxt`
+        if (c + 1 < c_end) issue(c + 1, nxt);
+        const int nv = nval(c);
+        if (nv == kC)
+            state4_step<MODE, true>(cur, S, p.out + obase(c), orow, kC, wave, lane, phi_cols, kt_lane);
+        else
+            state4_step<MODE, false>(cur, S, p.out + obase(c), orow, nv, wave, lane, phi_cols, kt_lane);
+    };
+
+    if (c_begin < c_end) issue(c_begin, buf0);
+    for (int c = c_begin; c < c_end; c += 2) {
+        step(c, buf0, buf1);
+        if (c + 1 < c_end) step(c + 1, buf1, buf0);
+    }
+
+    if constexpr (MODE == kModeOut) {
+        if (grp != ngroups - 1) return;
+        float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n] = S[r][nt][i];
+    } else if (phi_cols) {
+        // phi as A fragments, transposed 16x16 tile by tile through this
+        // wave's V area of buffer 0 (unused by identity columns).
+        lds_barrier();  // every wave is done with the last chunk's buffers
+        uint16_t* Ph = sg.phi + group_unit(sg, p.H, sidx, h, grp) * kDK * kDK;
+        lds_u16* tt = reinterpret_cast<lds_u16*>(buf0 + St::offV + wave * 4 * kFragB);
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int T = (col0_wave - dv) / 16 + nt;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) tt[(4 * g + i) * 16 + n] = f2bf_bits(S[r][nt][i]);
+                if (lane < 32) {  // fragment lanes 16 (2 (T % 2) + h2) + n: row n of the tile, columns 8 h2 ..
+                    const int h2 = lane >> 4;
+                    const u32x4 v = *reinterpret_cast<const lds_u32x4*>(tt + n * 16 + 8 * h2);
+                    *reinterpret_cast<u32x4*>(Ph + ((r * 4 + (T >> 1)) * 64 + 16 * (2 * (T & 1) + h2) + n) * 8) = v;
+                }
+            }
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            f32x4* Ps = reinterpret_cast<f32x4*>(sg.psi +
+                                                 (group_unit(sg, p.H, sidx, h, grp) * (dv / 16) + col0_wave / 16 + nt) * 2048);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) Ps[r * 64 + lane] = S[r][nt];
+        }
+    }
+}
+
 // Initial states of the chunk groups: S_in(0) = state_in (or 0) and
 // S_in(j + 1) = phi_j S_in(j) + psi_j, written over psi_j.  One workgroup of
 // 8 waves per (sequence-head, 16-column tile); wave w owns accumulator row
@@ -1302,9 +1732,7 @@ __global__ void gdn_fill_zero_kernel(float* __restrict__ p, size_t n) {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-constexpr size_t kBytesT = 8 * 64 * 16;  // Tp fragments
-constexpr size_t kBytesA = 6 * 64 * 16;  // nonzero Aq fragments
-constexpr size_t kBytesG = 256 * 4;      // gate block
+constexpr size_t kBytesRec = kRecFrags * 64 * 16;  // one (chunk, head) record
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -1314,6 +1742,7 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 // through the groups' affine maps).
 struct StatePlan {
     int NT_out, NW_out, nvg_out, NT_map, NW_map, nvg_map, G;
+    bool wide;  // dv % 128 == 0: gdn_prefill_state4_kernel (4 waves x 32 columns, 128 columns a workgroup)
 };
 
 // `exact`: max_chunks is the exact chunk count of every sequence, so the
@@ -1321,6 +1750,20 @@ struct StatePlan {
 // untrimmed count, which never decreases as sequences grow.
 StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact) {
     StatePlan s;
+    s.wide = dv % 128 == 0;
+    if (s.wide) {
+        s.NT_out = s.NT_map = 2;
+        s.NW_out = s.NW_map = 4;
+        s.nvg_out = dv / 128;
+        s.nvg_map = (dv + kDK) / 128;
+        const long long base = nheads * s.nvg_out;  // output-pass workgroups (one per CU) with one group
+        long long G = 1;
+        if (base < 256 && max_chunks >= 8)
+            G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
+        if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
+        s.G = G < 2 ? 1 : static_cast<int>(G);
+        return s;
+    }
     // Two waves per SIMD (8-wave workgroups) where the tiling allows: the
     // waves hide each other's LDS and copy latency.  The output pass then
     // uses 16-column waves, the map pass 32-column waves, both within 256
@@ -1366,7 +1809,7 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
 }
 
 struct WsLayout {
-    size_t offT, offA, offG, offPsi, offPhi, offPlan, total;
+    size_t offR, offPsi, offPhi, offPlan, total;
 };
 
 // Packed sequences with chunk groups plan them per sequence on the device
@@ -1379,10 +1822,8 @@ WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const State
     const size_t ch = static_cast<size_t>(slots) * H;
     const bool planned = planned_groups(sp, varlen);
     WsLayout L;
-    L.offT = 0;
-    L.offA = align256(L.offT + ch * kBytesT);
-    L.offG = align256(L.offA + ch * kBytesA);
-    L.offPsi = align256(L.offG + ch * kBytesG);
+    L.offR = 0;
+    L.offPsi = align256(L.offR + ch * kBytesRec);
     const size_t units = planned      ? static_cast<size_t>(H) * plan_target(sp, H)
                          : sp.G > 1 ? static_cast<size_t>(nheads) * sp.G
                                     : 0;
@@ -1400,6 +1841,17 @@ int check_common(const char* who, int H, int dk, int dv) {
         return fail(GDN_ERR_UNSUPPORTED, "%s: dv=%d must be a multiple of 16 in [16, 512]", who, dv);
     return GDN_OK;
 }
+
+template <int MODE>
+int launch_state4(const PrefillParams& p, const StateGrid& sg, hipStream_t stream) {
+    const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups_run * sg.nvg;
+    if (nwg > 0x7fffffffLL) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
+    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE>), dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p, sg);
+    return gdn_host::check_launch(MODE == kModeMap ? "gdn_prefill_state4_kernel<map>" : "gdn_prefill_state4_kernel");
+}
+
+template <int MODE>
+int launch_state_plan(const PrefillParams& p, const StateGrid& sg, const StatePlan& sp, hipStream_t stream);
 
 template <int MODE, int NT>
 int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_t stream) {
@@ -1428,6 +1880,17 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
     return gdn_host::check_launch(MODE == kModeMap ? "gdn_prefill_state_kernel<map>" : "gdn_prefill_state_kernel");
 }
 
+template <int MODE>
+int launch_state_plan(const PrefillParams& p, const StateGrid& sg, const StatePlan& sp, hipStream_t stream) {
+    if (sp.wide) return launch_state4<MODE>(p, sg, stream);
+    if (MODE == kModeMap)
+        return sp.NT_map == 4   ? launch_state<MODE, 4>(p, sg, sp.NW_map, stream)
+               : sp.NT_map == 2 ? launch_state<MODE, 2>(p, sg, sp.NW_map, stream)
+                                : launch_state<MODE, 1>(p, sg, sp.NW_map, stream);
+    return sp.NT_out == 2 ? launch_state<MODE, 2>(p, sg, sp.NW_out, stream)
+                          : launch_state<MODE, 1>(p, sg, sp.NW_out, stream);
+}
+
 // phases: bit 0 = chunk-parallel intra kernel, bit 1 = state pass (map pass
 // and scan when chunk groups are used, then the output pass).
 int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* workspace, size_t ws_bytes,
@@ -1442,9 +1905,7 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     if (!gdn_host::aligned(workspace, 256))
         return fail(GDN_ERR_INVALID_ARGUMENT, "prefill: workspace must be 256-byte aligned");
     char* ws = static_cast<char*>(workspace);
-    p.wsT = reinterpret_cast<u32x4*>(ws + L.offT);
-    p.wsA = reinterpret_cast<u32x4*>(ws + L.offA);
-    p.wsG = reinterpret_cast<float*>(ws + L.offG);
+    p.wsR = reinterpret_cast<u32x4*>(ws + L.offR);
 
     p.xcd_heads = (nheads % 8 == 0) ? 1 : 0;
     p.nchunk_grid = nchunk_grid;
@@ -1487,9 +1948,7 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
             sm.nheads = p.H;  // grid: (head, map slot, column part)
             sm.nvg = sp.nvg_map;
             sm.ngroups_run = map_cap;
-            st = sp.NT_map == 4   ? launch_state<kModeMap, 4>(p, sm, sp.NW_map, stream)
-                 : sp.NT_map == 2 ? launch_state<kModeMap, 2>(p, sm, sp.NW_map, stream)
-                                  : launch_state<kModeMap, 1>(p, sm, sp.NW_map, stream);
+            st = launch_state_plan<kModeMap>(p, sm, sp, stream);
             if (st != GDN_OK) return st;
             const long long nscan = nheads * (p.dv / 16);
             if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
@@ -1500,15 +1959,12 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
         so.nheads = p.H;  // grid: (head, slot, column part)
         so.nvg = sp.nvg_out;
         so.ngroups_run = target;
-        return sp.NT_out == 2 ? launch_state<kModeOut, 2>(p, so, sp.NW_out, stream)
-                              : launch_state<kModeOut, 1>(p, so, sp.NW_out, stream);
+        return launch_state_plan<kModeOut>(p, so, sp, stream);
     }
     if (sp.G > 1) {
         sg.nvg = sp.nvg_map;
         sg.ngroups_run = sp.G - 1;
-        st = sp.NT_map == 4   ? launch_state<kModeMap, 4>(p, sg, sp.NW_map, stream)
-             : sp.NT_map == 2 ? launch_state<kModeMap, 2>(p, sg, sp.NW_map, stream)
-                              : launch_state<kModeMap, 1>(p, sg, sp.NW_map, stream);
+        st = launch_state_plan<kModeMap>(p, sg, sp, stream);
         if (st != GDN_OK) return st;
         const long long nscan = nheads * (p.dv / 16);
         if (nscan > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
@@ -1517,8 +1973,7 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
     }
     sg.nvg = sp.nvg_out;
     sg.ngroups_run = sp.G;
-    return sp.NT_out == 2 ? launch_state<kModeOut, 2>(p, sg, sp.NW_out, stream)
-                          : launch_state<kModeOut, 1>(p, sg, sp.NW_out, stream);
+    return launch_state_plan<kModeOut>(p, sg, sp, stream);
 }
 
 }  // namespace

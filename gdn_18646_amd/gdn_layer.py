@@ -153,7 +153,8 @@ class GDNLayerCustom:
         if not return_state:
             return y
         nc = self.CK - 1
-        xn_hist = torch.cat([st.get('xn', torch.zeros(B, nc, Dd, dtype=x.dtype, device=x.device)), xn], 1)[:, -nc:]
+        h = torch.cat([st.get('xn', torch.zeros(B, nc, Dd, dtype=x.dtype, device=x.device)), xn], 1)
+        xn_hist = h[:, h.shape[1] - nc:]  # the last nc tokens ([:, -nc:] would keep all of them for nc = 0)
         return y, dict(recurrent=S, conv_q=outs[5], conv_k=outs[6], conv_v=outs[7], xn=xn_hist.contiguous())
 
     @torch.no_grad()

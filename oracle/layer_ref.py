@@ -11,7 +11,7 @@ import torch
 
 from .decode_ref import ref_decode
 from .prefill_ref import ref_prefill
-from .proj_ref import ref_proj_conv_silu
+from .proj_ref import ref_proj_conv_silu, ref_proj_conv_silu_f32
 from .rmsnorm_ref import ref_rmsnorm
 
 
@@ -48,6 +48,21 @@ def decode_conv_step(xn, W, conv_w, conv_state):
     return torch.nn.functional.silu(conv).to(xn.dtype), window[:, :, 1:].contiguous()
 
 
+def decode_conv_step_f32(xn, W, conv_w, conv_state):
+    """decode_conv_step with the projection kept in float32 through the conv.
+
+    These are the rounding points of the reference's CUDA projection kernel,
+    which holds P in fp32 before the conv (kernels/fused_proj_conv_silu.cu:250-290):
+    the window is the cached bf16 projections (widened) plus the new fp32
+    one, the tap sum is fp32, and the cache receives bf16(P).
+    """
+    proj = xn.squeeze(1).float() @ W.float().T
+    window = torch.cat([conv_state.float(), proj.unsqueeze(-1)], dim=-1)
+    conv = (window * conv_w.float().unsqueeze(0)).sum(dim=-1)
+    cache = torch.cat([conv_state, proj.to(xn.dtype).unsqueeze(-1)], dim=-1)[:, :, 1:]
+    return torch.nn.functional.silu(conv).to(xn.dtype), cache.contiguous()
+
+
 def dt_bias_per_head(dt_bias, H):
     """Scalar dt_bias expanded to [H] (gdn_layer.py:72-76)."""
     if dt_bias.numel() == 1:
@@ -56,20 +71,32 @@ def dt_bias_per_head(dt_bias, H):
 
 
 class GDNLayerBaseline:
-    """Pure-PyTorch GDN layer (gdn_layer.py:108-200)."""
+    """Pure-PyTorch GDN layer (gdn_layer.py:108-200).
 
-    def __init__(self, weights, chunk_size=None):
+    ``fp32_proj=True`` keeps the q/k/v projections in float32 through the
+    conv and SiLU (ref_proj_conv_silu_f32, decode_conv_step_f32): the
+    rounding points of the reference's CUDA projection kernel and of this
+    build's kernels; the default follows the reference's PyTorch baseline,
+    which rounds the projection to bf16 before the conv.
+    """
+
+    def __init__(self, weights, chunk_size=None, fp32_proj=False):
         self.w = weights
         self.D, self.H, self.DK, self.DV, self.CK = dims(weights)
         self.scale = self.DK ** -0.5
         self.chunk_size = chunk_size
+        self.fp32_proj = fp32_proj
 
     def init_decode_state(self, B, device=None):
         return zero_decode_state(self.w, B, device=device)
 
     @torch.no_grad()
-    def forward(self, x, mask=None):
-        """x [B, T, D] bf16 -> [B, T, D] bf16 (gdn_layer.py:120-158)."""
+    def forward(self, x, mask=None, return_state=False):
+        """x [B, T, D] bf16 -> [B, T, D] bf16 (gdn_layer.py:120-158).
+
+        ``return_state`` also returns the final recurrent state [B, H, DK, DV]
+        (the reference discards it, gdn_layer.py:256).
+        """
         B, T, _ = x.shape
         D, H, DK, DV = self.D, self.H, self.DK, self.DV
         w = self.w
@@ -77,17 +104,20 @@ class GDNLayerBaseline:
             mask = x.new_ones(B, T, dtype=torch.float32)
         xn = ref_rmsnorm(x.reshape(B * T, D), w['norm_gamma']).reshape(B, T, D)
 
+        pcs = ref_proj_conv_silu_f32 if self.fp32_proj else ref_proj_conv_silu
+
         def proj(W, cw, dh):
-            return ref_proj_conv_silu(xn, W, cw).reshape(B, T, H, dh).transpose(1, 2).contiguous()
+            return pcs(xn, W, cw).reshape(B, T, H, dh).transpose(1, 2).contiguous()
 
         q = proj(w['W_q'], w['conv_q'], DK)
         k = proj(w['W_k'], w['conv_k'], DK)
         v = proj(w['W_v'], w['conv_v'], DV)
         a = (xn @ w['W_a'].T).transpose(1, 2).contiguous()
         b = (xn @ w['W_b'].T).transpose(1, 2).contiguous()
-        o, _ = ref_prefill(q, k, v, w['A_log'], a, w['dt_bias'], b, mask,
+        o, S = ref_prefill(q, k, v, w['A_log'], a, w['dt_bias'], b, mask,
                            state_in=None, scale=self.scale, chunk_size=self.chunk_size)
-        return o.to(x.dtype).transpose(1, 2).reshape(B, T, H * DV) @ w['W_o'].T
+        y = o.to(x.dtype).transpose(1, 2).reshape(B, T, H * DV) @ w['W_o'].T
+        return (y, S) if return_state else y
 
     @torch.no_grad()
     def decode(self, x, state=None):
@@ -99,9 +129,10 @@ class GDNLayerBaseline:
         if state is None:
             state = self.init_decode_state(B, device=x.device)
         xn = ref_rmsnorm(x.reshape(B, D), w['norm_gamma']).reshape(B, 1, D)
-        qp, conv_q = decode_conv_step(xn, w['W_q'], w['conv_q'], state['conv_q'])
-        kp, conv_k = decode_conv_step(xn, w['W_k'], w['conv_k'], state['conv_k'])
-        vp, conv_v = decode_conv_step(xn, w['W_v'], w['conv_v'], state['conv_v'])
+        step = decode_conv_step_f32 if self.fp32_proj else decode_conv_step
+        qp, conv_q = step(xn, w['W_q'], w['conv_q'], state['conv_q'])
+        kp, conv_k = step(xn, w['W_k'], w['conv_k'], state['conv_k'])
+        vp, conv_v = step(xn, w['W_v'], w['conv_v'], state['conv_v'])
         xn_state = torch.cat([state['xn'], xn], dim=1)[:, 1:, :].contiguous()
         q = qp.reshape(B, 1, H, DK)
         k = kp.reshape(B, 1, H, DK)

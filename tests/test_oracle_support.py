@@ -101,3 +101,37 @@ def test_layer_decode_matches_prefill():
         outs.append(y_t)
     y_dec = torch.cat(outs, 1)
     torch.testing.assert_close(y_dec.float(), y_pre.float(), rtol=5e-2, atol=2e-2)
+
+
+def test_layer_fp32_proj_decode_matches_prefill():
+    """The fp32-projection layer variant: T decode steps equal one prefill (outputs
+    and the final recurrent state), as the reference's own layer check (bench_gdn.py:200-219)."""
+    w = _small_weights(seed=4)
+    layer = GDNLayerBaseline(w, chunk_size=16, fp32_proj=True)
+    x = torch.randn(2, 37, 64, generator=torch.Generator().manual_seed(5)).bfloat16()
+    y_pre, S_pre = layer.forward(x, return_state=True)
+    state = layer.init_decode_state(2)
+    outs = []
+    for t in range(37):
+        y_t, state = layer.decode(x[:, t:t + 1], state)
+        outs.append(y_t)
+    torch.testing.assert_close(torch.cat(outs, 1).float(), y_pre.float(), rtol=2e-2, atol=2e-2)
+    rel = ((state["recurrent"] - S_pre).norm() / S_pre.norm()).item()
+    assert rel < 1e-2, rel
+
+
+def test_decode_conv_step_f32_vs_brute_force():
+    """One decode conv step equals the last row of the fp64 brute-force projection + conv
+    + SiLU over the cached window; the cache shifts in bf16(P)."""
+    from oracle.layer_ref import decode_conv_step_f32
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 4, 64, generator=g).bfloat16()
+    W = (torch.randn(40, 64, generator=g) * 64 ** -0.5).bfloat16()
+    cw = (torch.randn(40, 4, generator=g) * 0.5).bfloat16()
+    cache = (x[:, :3].float() @ W.float().T).bfloat16().transpose(1, 2).contiguous()  # [B, 40, 3]
+    y, new_cache = decode_conv_step_f32(x[:, 3:4], W, cw, cache)
+    P = torch.cat([cache.double(), (x[:, 3].double() @ W.double().T).unsqueeze(-1)], -1)
+    conv = (P * cw.double().unsqueeze(0)).sum(-1)
+    torch.testing.assert_close(y.double(), conv * torch.sigmoid(conv), rtol=1e-2, atol=1e-3)
+    assert torch.equal(new_cache[:, :, :2], cache[:, :, 1:])
+    assert torch.equal(new_cache[:, :, 2], (x[:, 3].float() @ W.float().T).bfloat16())

@@ -180,14 +180,37 @@ def test_prefill_token_major_output(exts, dev, B, H, T, dv):
 
 
 def test_prefill_varlen_chunk_groups(exts, dev):
-    """Packed sequences of very different lengths with chunk groups: the short
-    ones leave most of their groups empty (identity maps).  Slow decay, as above."""
+    """Packed sequences of very different lengths with chunk groups planned per
+    sequence (lengths 3000, 10, 700, 0, 1500 at H=2 give group lengths of 4
+    chunks and no empty group).  Slow decay."""
     lengths = [3000, 10, 700, 0, 1500]
     d = synth.varlen_inputs(lengths, 2, 128, 64, seed=11)
     d["A_log"] = torch.tensor([-8.0, -3.0])
     g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
     out, S = exts["prefill"].prefill_varlen(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"],
                                             g["cu_seqlens"], g["state_in"], 0.0)
+    torch.cuda.synchronize()
+    o_ref, S_ref = ref_prefill_varlen(d["q"], d["k"], d["v"], d["A_log"], d["a"], 0.0, d["b_logits"],
+                                      d["cu_seqlens"], state_in=d["state_in"], chunk_size=64)
+    assert_out_close(out.cpu(), o_ref)
+    for i in range(len(lengths)):
+        assert_state_close(S[i].cpu(), S_ref[i], what=f"state of sequence {i}")
+
+
+@pytest.mark.parametrize("dv", [64, 128])
+def test_prefill_varlen_group_cap_binds(exts, dev, dv):
+    """The 16-group cap binds: a 6400-token sequence (100 chunks) at H=2 gets 16
+    groups of ceil(100 / 16) = 7 chunks, so its last group is empty.  That
+    group's output pass runs no chunk and writes state_out from the scan's
+    result; the scan composes 15 steps (the map pass of group 14 covers 2
+    chunks).  Nonzero initial states; dv = 64 (16-column kernel) and 128
+    (32-column kernel)."""
+    lengths = [6400, 100]
+    d = synth.varlen_inputs(lengths, 2, 128, dv, seed=13)
+    d["A_log"] = torch.tensor([-6.0, -2.0])
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    out, S = exts["prefill"].prefill_varlen(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"],
+                                            d["cu_seqlens"], g["state_in"], 0.0)
     torch.cuda.synchronize()
     o_ref, S_ref = ref_prefill_varlen(d["q"], d["k"], d["v"], d["A_log"], d["a"], 0.0, d["b_logits"],
                                       d["cu_seqlens"], state_in=d["state_in"], chunk_size=64)
