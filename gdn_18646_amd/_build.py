@@ -32,6 +32,12 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags.  prefill.hip: MFMA results in VGPRs -- its state
+# kernels post-process every accumulator on the VALU, and with one wave per
+# SIMD the compiler's default parks them in AGPRs and copies them back.
+EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _run(cmd):
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(ln for ln in r.stdout.splitlines() if "packed-fp32-ops" not in ln)
@@ -44,7 +50,8 @@ def build_library(jobs=None):
     """Compile every HIP source for gfx950 and link libgdn_amd.so."""
     os.makedirs(BUILD, exist_ok=True)
     objs = [os.path.join(BUILD, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
-    cmds = [[HIPCC, *HIPCC_FLAGS, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(HIP_SOURCES, objs)]
+    cmds = [[HIPCC, *HIPCC_FLAGS, *EXTRA_FLAGS.get(s, []), "-c", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(HIP_SOURCES, objs)]
     jobs = jobs or min(len(cmds), os.cpu_count() or 1, 8)
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
         list(ex.map(_run, cmds))

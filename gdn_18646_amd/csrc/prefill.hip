@@ -1103,25 +1103,36 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2b: the state pass for dv % 128 == 0 -- four waves of 32 columns
+// Kernel 2b: the state pass for dv % 128 == 0 -- four compute waves of 32
+// columns and one copy wave
 // ---------------------------------------------------------------------------
-// A workgroup owns 128 state columns of one (sequence, head, chunk group);
-// wave w owns columns 32 w .. 32 w + 31 as two 16-column MFMA tiles, so every
-// operand fragment it reads from LDS feeds two MFMAs.  (With 16-column waves,
-// eight per CU, the LDS reads of a chunk step outlast its MFMAs.)  The output
-// pass runs one workgroup per CU, one wave per SIMD with the whole register
-// file; the map pass two workgroups per CU.
+// A workgroup owns 128 state columns of one (sequence, head, chunk group):
+// compute wave w owns columns 32 w .. 32 w + 31 as two 16-column MFMA tiles,
+// so every operand fragment it reads from LDS feeds two MFMAs (with 16-column
+// waves, eight per CU, the LDS reads of a chunk step outlast its MFMAs).
+// In the output pass three copy waves do all global memory traffic of the
+// chunk loop: waves 4 and 5 stage chunk c + 1 (half of the copies each)
+// while the compute waves work on chunk c, and wave 6 writes chunk c - 1's
+// outputs, which the compute waves left in LDS, as whole 256-byte rows.  The
+// pass is bound by memory traffic (77 KiB a chunk step): one wave keeps at
+// most ~63 copies in flight, so its rate is capped by memory latency; loads
+// and stores from separate waves flow at the same time; and no compute wave
+// stalls on a full memory queue.  The output pass runs one workgroup per CU
+// (one compute wave per SIMD), the map pass two.
 // Per chunk, DMA-staged into one of two LDS buffers:
 //   K   16 fragments, lane slots swizzled (kslot) for the K^T transposing reads
 //   Q   16 fragments (output pass)
 //   record: Tp 6, Aq 6 (output pass), gate block 1
-//   V   wave w's [64 rows][32 columns] bf16 at offV + 4 KiB w (not for phi columns)
-// Wave w copies a fixed share: K and Q fragments 4 w .. 4 w + 3 (row block w),
-// record fragments w, w + 4, w + 8, w + 12, and its own V columns.  Full chunks
-// take a path without per-row checks; a sequence's partial last chunk clamps
-// its copies to the sequence and predicates its output stores.  Rows past the
-// sequence end stay finite copies of the last row, and their Tp rows and
-// columns are zero (beta m = 0 there), so they add exact zeros.
+//   V   compute wave w's [64 rows][32 columns] bf16 at offV + 4 KiB w (not
+//       for phi columns)
+// and in the output pass two output tiles [64 rows][128 columns] bf16 (row
+// pitch 272 bytes: the compute waves' 8-byte writes then hit all 64 banks).
+// Full chunks take a path without per-row checks; a sequence's partial last
+// chunk clamps its copies to the sequence and predicates its output rows.
+// Rows past the sequence end stay finite copies of the last row, and their Tp
+// rows and columns are zero (beta m = 0 there), so they add exact zeros.
+constexpr int kObPitch = 272;                // output tile row pitch (bytes)
+constexpr int kObBytes = kC * kObPitch;      // one output tile
 template <int MODE>
 struct Stage4 {
     static constexpr bool out = MODE == kModeOut;
@@ -1134,7 +1145,11 @@ struct Stage4 {
     static constexpr int offG = offR + (out ? kRecG : 6) * kFragB;
     static constexpr int offV = offR + nRec * kFragB;
     static constexpr int bytes = offV + 16 * kFragB;
-    static constexpr int stores = out ? 8 : 0;  // output stores per chunk per wave
+    static constexpr int ob_bytes = out ? kObBytes : 0;
+    // waves: 4 compute, then (output pass) 2 copying chunks in and a store wave
+    static constexpr int loaders = out ? 2 : 0;
+    static constexpr int nWaves = 4 + loaders + (out ? 1 : 0);
+    static constexpr int nStores = out ? kC * 256 / kFragB : 0;  // output store instructions per chunk
 };
 
 // Per-lane byte offsets of the copies (fixed for the kernel).
@@ -1142,70 +1157,86 @@ struct Lane4 {
     uint32_t k, q, r, v;
 };
 
-// Issue chunk `c`'s copies of this wave into `buf`.  `row0`: q/k/v row of the
-// chunk's first token; `rec`: the chunk's record; `vcol0`: this wave's first
-// V column.
-template <int MODE, bool FULL>
+// Issue chunk `c`'s copies into `buf`: jobs first, first + STRIDE, ... of
+// each kind (the output pass's copy wave takes all of them, STRIDE 1; in the
+// map pass each compute wave takes a quarter, STRIDE 4).  `row0`: q/k/v row
+// of the chunk's first token; `rec`: the chunk's record; `vcol0`: the
+// workgroup's first V column.
+template <int MODE, bool FULL, int STRIDE>
 __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf, size_t row0, const u32x4* rec,
-                                             int vcol0, int nvalid, int wave, int lane, const Lane4& L, bool v_on) {
+                                             int vcol0, int nvalid, int first, int lane, const Lane4& L, bool v_on) {
     using St = Stage4<MODE>;
-    // Full chunks: base at this wave's row block, fixed lane offsets.  The
-    // partial chunk: base at the chunk's first row and each lane's row
-    // clamped to the sequence, so every offset is non-negative and in range.
+    // Full chunks: uniform bases, fixed lane offsets.  The partial chunk:
+    // base at the chunk's first row and each lane's row clamped to the
+    // sequence, so every offset is non-negative and in range.
     const unsigned char* kc = reinterpret_cast<const unsigned char*>(p.k + row0 * kDK);
     const unsigned char* qc = reinterpret_cast<const unsigned char*>(p.q + row0 * kDK);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        lds_u8* kd = buf + St::offK + (4 * wave + s) * kFragB;
+    for (int i = 0; i < 16 / STRIDE; ++i) {  // fragment f = 4 mt + s: rows 16 mt.., k 32 s..
+        const int f = first + STRIDE * i, mt = f >> 2, s = f & 3;
         if (FULL) {
-            dma16(kc + 16 * wave * kDK * 2 + 64 * s, L.k, kd);
+            dma16(kc + mt * 16 * kDK * 2 + 64 * s, L.k, buf + St::offK + f * kFragB);
         } else {
-            const int row = min(16 * wave + kslot_row(lane), nvalid - 1);
-            dma16(kc, static_cast<uint32_t>((row * kDK + 32 * s + 8 * (lane >> 4)) * 2), kd);
+            const int row = min(16 * mt + kslot_row(lane), nvalid - 1);
+            dma16(kc, static_cast<uint32_t>((row * kDK + 32 * s + 8 * (lane >> 4)) * 2), buf + St::offK + f * kFragB);
         }
     }
     if constexpr (St::out) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            lds_u8* qd = buf + St::offQ + (4 * wave + s) * kFragB;
+        for (int i = 0; i < 16 / STRIDE; ++i) {
+            const int f = first + STRIDE * i, mt = f >> 2, s = f & 3;
             if (FULL) {
-                dma16(qc + 16 * wave * kDK * 2 + 64 * s, L.q, qd);
+                dma16(qc + mt * 16 * kDK * 2 + 64 * s, L.q, buf + St::offQ + f * kFragB);
             } else {
-                const int row = min(16 * wave + (lane & 15), nvalid - 1);
-                dma16(qc, static_cast<uint32_t>((row * kDK + 32 * s + 8 * (lane >> 4)) * 2), qd);
+                const int row = min(16 * mt + (lane & 15), nvalid - 1);
+                dma16(qc, static_cast<uint32_t>((row * kDK + 32 * s + 8 * (lane >> 4)) * 2),
+                      buf + St::offQ + f * kFragB);
             }
         }
     }
     const unsigned char* rb = reinterpret_cast<const unsigned char*>(rec);
 #pragma unroll
-    for (int j0 = 0; j0 < St::nRec; j0 += 4) {
-        const int j = j0 + wave;
+    for (int i = 0; i < (St::nRec + STRIDE - 1) / STRIDE; ++i) {
+        const int j = first + STRIDE * i;
         if (j < St::nRec) {
             const int src = St::out ? j : (j < 6 ? j : kRecG);
             dma16(rb + src * kFragB, L.r, buf + St::offR + j * kFragB);
         }
     }
-    if (v_on) {
+    if (v_on) {  // job u: compute wave u / 4's columns, rows 16 (u % 4) ..
         const unsigned char* vb = reinterpret_cast<const unsigned char*>(p.v + row0 * p.dv + vcol0);
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            lds_u8* vd = buf + St::offV + wave * 4 * kFragB + it * kFragB;
+        for (int i = 0; i < 16 / STRIDE; ++i) {
+            const int u = first + STRIDE * i, w = u >> 2, it = u & 3;
+            lds_u8* vd = buf + St::offV + u * kFragB;
             if (FULL) {
-                dma16(vb + static_cast<size_t>(16 * it) * p.dv * 2, L.v, vd);
+                dma16(vb + static_cast<size_t>(16 * it) * p.dv * 2 + 64 * w, L.v, vd);
             } else {
                 const int row = min(16 * it + (lane >> 2), nvalid - 1);
-                dma16(vb, static_cast<uint32_t>((row * p.dv + 8 * (lane & 3)) * 2), vd);
+                dma16(vb, static_cast<uint32_t>((row * p.dv + 32 * w + 8 * (lane & 3)) * 2), vd);
             }
         }
     }
 }
 
+// The copy wave: chunk c's output tile from LDS to `ob` (row 0, the
+// workgroup's first column), 4 rows of 256 bytes per instruction.
+template <bool FULL>
+__device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, int orow, int nvalid, int lane) {
+#pragma unroll
+    for (int i = 0; i < kC / 4; ++i) {
+        const int row = 4 * i + (lane >> 4);
+        const u32x4 v = *reinterpret_cast<const lds_u32x4*>(obuf + row * kObPitch + (lane & 15) * 16);
+        if (FULL || row < nvalid) *reinterpret_cast<u32x4*>(ob + static_cast<size_t>(row) * orow + (lane & 15) * 8) = v;
+    }
+}
+
 // One chunk of the state recurrence for this wave's 128 x 32 state tile, the
-// chunk's operands staged in `buf`.  `ob`: out row of the chunk's first
-// token at this wave's first column (uniform).
-template <int MODE, bool FULL>
-__device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2], uint16_t* ob, int orow, int nvalid,
-                                            int wave, int lane, bool v_zero, uint32_t kt_lane) {
+// chunk's operands staged in `buf`; the output pass leaves the chunk's
+// outputs in the LDS tile `obuf` for the copy wave.
+template <int MODE>
+__device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2], lds_u8* obuf, int wave, int lane,
+                                            bool v_zero, uint32_t kt_lane) {
     using St = Stage4<MODE>;
     constexpr bool OUT = St::out;
     const int n = lane & 15, g = lane >> 4;
@@ -1215,14 +1246,11 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
     // (a) X = K S and P^T = S^T Q^T.  The state's bf16 copy is the B operand
     //     of K S and the A operand of S^T Q^T as it stands (k = state rows
     //     32 s + 8 g + j in both).
-    // The map pass runs two waves per SIMD within 256 registers: phase fences
-    // (PHASE()) keep the scheduler from hoisting every fragment read of the
-    // step to its top; the other wave covers the latency.  The output pass
-    // (one wave per SIMD, 512 registers) lets the reads run ahead.
-#define PHASE()                                        \
-    do {                                               \
-        if constexpr (!OUT) __builtin_amdgcn_sched_barrier(0); \
-    } while (0)
+    // Phase fences (PHASE()) keep the scheduler from hoisting every fragment
+    // read of the step to its top: a wave then stays within the 256
+    // architectural VGPRs, and no accumulator round-trips through AGPRs each
+    // time the VALU touches it.
+#define PHASE() __builtin_amdgcn_sched_barrier(0)
     const float gC = G[kC - 1];
     f32x4 X[4][2], P[4][2];
 #pragma unroll
@@ -1323,7 +1351,8 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
             S[r][nt] = mfma16x16x32(ktf[r][1], BS1[nt], S[r][nt]);
         }
     // (e) O^T = (m scale gamma) o P^T + dV^T Aq^T: each lane holds 4
-    //     consecutive output columns of token 16 mt + n, stored as 8 bytes.
+    //     consecutive output columns of token 16 mt + n, written to the
+    //     output tile as 8 bytes.
     if constexpr (OUT) {
         bf16x8 af[6];
 #pragma unroll
@@ -1340,11 +1369,9 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
             O[2] = mfma16x16x32(BD1, af[3], mfma16x16x32(BD0, af[2], co[2] * P[2][nt]));
             O[3] = mfma16x16x32(BD1, af[5], mfma16x16x32(BD0, af[4], co[3] * P[3][nt]));
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const int row = 16 * mt + n;
-                if (FULL || row < nvalid)
-                    *reinterpret_cast<u32x2*>(ob + row * orow + 16 * nt + 4 * g) = pack4_bf16(O[mt]);
-            }
+            for (int mt = 0; mt < 4; ++mt)
+                *reinterpret_cast<lds_u32x2*>(obuf + (16 * mt + n) * kObPitch + (32 * wave + 16 * nt + 4 * g) * 2) =
+                    pack4_bf16(O[mt]);
         }
     }
 #undef PHASE
@@ -1354,14 +1381,21 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 // chunk group) in the roles of gdn_prefill_state_kernel (output pass: from
 // the group's initial state, outputs and the final state; map pass: psi
 // columns from zero with V, phi columns from the identity without V).
+// This file is compiled with MFMA results forced into VGPRs (the build's
+// -amdgpu-mfma-vgpr-form): with one compute wave per SIMD the compiler would
+// otherwise park the accumulators in AGPRs and copy them back for every VALU
+// use, about 300 extra instructions per chunk.
+// The output pass adds the copy waves.  In the map pass (two workgroups per
+// CU, 39 KiB a chunk step each) the compute waves issue a quarter of the
+// copies each: dedicated copy waves there measured slower.
 template <int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == kModeOut ? 1 : 2,
-                                                                      MODE == kModeOut ? 1 : 2))) void
-gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
+__global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_waves_per_eu(
+    MODE == kModeOut ? 1 : 2, 2))) void gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
     using St = Stage4<MODE>;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2][St::bytes];
-    lds_u8* const buf0 = (lds_u8*)&smem[0][0];
-    lds_u8* const buf1 = (lds_u8*)&smem[1][0];
+    constexpr bool OUT = St::out;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * St::bytes + 2 * St::ob_bytes];
+    auto buf = [&](int i) { return (lds_u8*)&smem[0] + i * St::bytes; };
+    auto obuf = [&](int i) { return (lds_u8*)&smem[0] + 2 * St::bytes + i * St::ob_bytes; };
 
     const int wg = blockIdx.x;
     int head, grp, vg, ngroups;
@@ -1391,12 +1425,19 @@ gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
     const int h = head % p.H;
     const SeqInfo sq = seq_info(p, sidx);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Copy waves (output pass): 4 and 5 copy chunk c + 1 in, 6 writes chunk
+    // c - 1's outputs.  In the map pass the compute waves copy (`issuer`).
+    const bool loader = OUT && wave >= 4 && wave < 4 + St::loaders;
+    const bool storer = OUT && wave == 4 + St::loaders;
+    const bool issuer = OUT ? loader : true;
+    const bool copier = loader || storer;
+    const int cw = copier ? 0 : wave;  // compute wave (column block)
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
     const int dv = p.dv;
-    const int col0_wave = vg * 128 + 32 * wave;  // map pass: >= dv means identity columns
+    const int col0_wave = vg * 128 + 32 * cw;  // map pass: >= dv means identity columns
     const bool phi_cols = MODE == kModeMap && vg * 128 >= dv;
-    const int vcol0 = phi_cols ? 0 : col0_wave;
+    const int vcol0 = phi_cols ? 0 : vg * 128;
     const int nchunks = (sq.len + kC - 1) / kC;
     const int glen = (nchunks + ngroups - 1) / ngroups;
     const int c_begin = min(grp * glen, nchunks), c_end = min(c_begin + glen, nchunks);
@@ -1407,7 +1448,10 @@ gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
 
     // State tile: S[r][nt][i] = S[rho(r, g, i)][col0_wave + 16 nt + n].
     f32x4 S[8][2];
-    if constexpr (MODE == kModeMap) {
+    if (copier) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) S[r][0] = S[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else if constexpr (MODE == kModeMap) {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
@@ -1441,46 +1485,52 @@ gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
     const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
     const int orow = p.out_tm ? p.H * dv : dv;
     auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
-    auto obase = [&](int c) {
+    auto obase = [&](int c) {  // out row of chunk c's first token, the workgroup's first column
         const size_t tok = static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + static_cast<size_t>(c) * kC;
-        return (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + col0_wave;
+        return p.out + (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + vg * 128;
     };
     auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
     auto rec = [&](int c) { return p.wsR + (static_cast<size_t>(sq.slot0 + c) * p.H + h) * kRecFrags * 64; };
-    auto issue = [&](int c, lds_u8* buf) {
-        // Opaque per call: otherwise the copies' LDS addresses (buffer, wave
-        // and fragment constants) are hoisted out of the chunk loop and held
-        // in SGPRs, which runs the output pass out of them.
-        int w = wave;
-        asm volatile("" : "+s"(w));
+    auto issue = [&](int c, int bi) {
+        // Opaque per call: otherwise the copies' LDS addresses (buffer and
+        // fragment constants) are hoisted out of the chunk loop and held in
+        // SGPRs, which runs the kernel out of them.
+        int first = OUT ? wave - 4 : wave;
+        asm volatile("" : "+s"(first));
+        lds_u8* b = buf(bi);
+        constexpr int STRIDE = OUT ? St::loaders : 4;
         if (nval(c) == kC)
-            stage4_issue<MODE, true>(p, buf, rows(c), rec(c), vcol0, kC, w, lane, L, !phi_cols);
+            stage4_issue<MODE, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
         else
-            stage4_issue<MODE, false>(p, buf, rows(c), rec(c), vcol0, nval(c), w, lane, L, !phi_cols);
-    };
-    auto step = [&](int c, lds_u8* cur, lds_u8* nxt) {
-        // Chunk c's copies went out before chunk c-1's output stores (the
-        // one partial chunk of a sequence is always its group's last).
-        if (c == c_begin)
-            wait_vm<0>();
-        else
-            wait_vm<St::stores>();
-        lds_barrier();  // chunk c staged by every wave; nobody still reads `nxt`
-        if (c + 1 < c_end) issue(c + 1, nxt);
-        const int nv = nval(c);
-        if (nv == kC)
-            state4_step<MODE, true>(cur, S, p.out + obase(c), orow, kC, wave, lane, phi_cols, kt_lane);
-        else
-            state4_step<MODE, false>(cur, S, p.out + obase(c), orow, nv, wave, lane, phi_cols, kt_lane);
+            stage4_issue<MODE, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
     };
 
-    if (c_begin < c_end) issue(c_begin, buf0);
-    for (int c = c_begin; c < c_end; c += 2) {
-        step(c, buf0, buf1);
-        if (c + 1 < c_end) step(c + 1, buf1, buf0);
+    // Chunk c = c_begin + k uses buffer k % 2 and output tile k % 2.  Barrier
+    // k opens step k: chunk c is staged, nobody reads buffer (k + 1) % 2 any
+    // more, and chunk c - 1's outputs are in tile (k - 1) % 2.
+    if (issuer && c_begin < c_end) issue(c_begin, 0);
+    for (int c = c_begin; c < c_end; ++c) {
+        const int k = c - c_begin;
+        if (issuer) wait_vm<0>();  // chunk c staged
+        lds_barrier();
+        if (issuer && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
+        // Chunk c - 1 is never a sequence's partial last chunk here.
+        if (storer && k >= 1) stage4_store<true>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
+        if (!copier) state4_step<MODE>(buf(k & 1), S, obuf(k & 1), cw, lane, phi_cols, kt_lane);
     }
 
-    if constexpr (MODE == kModeOut) {
+    if constexpr (OUT) {
+        lds_barrier();  // the last chunk's outputs are in LDS
+        if (copier) {
+            if (storer && c_end > c_begin) {
+                const int c = c_end - 1, k = c - c_begin;
+                if (nval(c) == kC)
+                    stage4_store<true>(obuf(k & 1), obase(c), orow, kC, lane);
+                else
+                    stage4_store<false>(obuf(k & 1), obase(c), orow, nval(c), lane);
+            }
+            return;
+        }
         if (grp != ngroups - 1) return;
         float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
@@ -1489,12 +1539,14 @@ gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
             for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n] = S[r][nt][i];
+    } else if (loader) {
+        return;
     } else if (phi_cols) {
         // phi as A fragments, transposed 16x16 tile by tile through this
-        // wave's V area of buffer 0 (unused by identity columns).
-        lds_barrier();  // every wave is done with the last chunk's buffers
+        // wave's V area of buffer 0 (unused by identity columns): no copy is
+        // in flight any more, and no other wave reads that area.
         uint16_t* Ph = sg.phi + group_unit(sg, p.H, sidx, h, grp) * kDK * kDK;
-        lds_u16* tt = reinterpret_cast<lds_u16*>(buf0 + St::offV + wave * 4 * kFragB);
+        lds_u16* tt = reinterpret_cast<lds_u16*>(buf(0) + St::offV + cw * 4 * kFragB);
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
@@ -1846,7 +1898,8 @@ template <int MODE>
 int launch_state4(const PrefillParams& p, const StateGrid& sg, hipStream_t stream) {
     const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups_run * sg.nvg;
     if (nwg > 0x7fffffffLL) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE>), dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p, sg);
+    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE>), dim3(static_cast<unsigned>(nwg)), dim3(64 * Stage4<MODE>::nWaves),
+                       0, stream, p, sg);
     return gdn_host::check_launch(MODE == kModeMap ? "gdn_prefill_state4_kernel<map>" : "gdn_prefill_state4_kernel");
 }
 
