@@ -101,7 +101,7 @@ std::tuple<Tensor, Tensor> prefill(Tensor q, Tensor k, Tensor v, Tensor A_log, T
 // cu_seqlens int32/int64 [N+1] on CPU or GPU; state_in [N, H, K, V] or empty.
 std::tuple<Tensor, Tensor> prefill_varlen(Tensor q, Tensor k, Tensor v, Tensor A_log, Tensor a, double dt_bias,
                                           Tensor b_logits, Tensor cu_seqlens, Tensor state_in, double scale,
-                                          std::optional<Tensor> mask_opt, int64_t max_seqlen) {
+                                          std::optional<Tensor> mask_opt, int64_t max_seqlen, bool token_major) {
     check_bf16(q, "q");
     check_bf16(k, "k");
     check_bf16(v, "v");
@@ -153,11 +153,12 @@ std::tuple<Tensor, Tensor> prefill_varlen(Tensor q, Tensor k, Tensor v, Tensor A
     } else {
         cu_dev = cu_host.to(at::kInt).pin_memory().to(q.device(), /*non_blocking=*/true);
     }
-    auto out = at::empty({1, H, Ttot, V}, q.options());
+    auto out = token_major ? at::empty({1, Ttot, H, V}, q.options()) : at::empty({1, H, Ttot, V}, q.options());
     auto state_out = at::empty({N, H, K, V}, q.options().dtype(at::kFloat));
     const size_t ws_bytes = gdn_prefill_varlen_workspace_bytes(N, H, Ttot, K, V);
     auto ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
-    GDN_CHECK_STATUS(gdn_prefill_varlen_hip(bf(q), bf(k), bf(v), A_log.data_ptr<float>(), bf(a),
+    auto fn = token_major ? &gdn_prefill_varlen_tm_hip : &gdn_prefill_varlen_hip;
+    GDN_CHECK_STATUS(fn(bf(q), bf(k), bf(v), A_log.data_ptr<float>(), bf(a),
                                             static_cast<float>(dt_bias), bf(b_logits), mask_ptr,
                                             cu_dev.data_ptr<int32_t>(), N, static_cast<int>(maxlen), sin_ptr,
                                             static_cast<float>(scale), bf_mut(out), state_out.data_ptr<float>(), H,
@@ -288,6 +289,52 @@ std::vector<Tensor> in_proj(Tensor xn, Tensor W_qkvab, Tensor conv_w_qkv, int64_
     return res;
 }
 
+// Packed sequences: xn [T_total, D] (or [1, T_total, D]) with host offsets
+// cu_seqlens [N + 1]; returns q, k [1, H, T_total, dk], v [1, H, T_total, dv],
+// a, b [1, H, T_total], plus new conv caches [N, H d, K - 1] when want_cache.
+// Caches in (optional): [N, H d, K - 1].
+std::vector<Tensor> in_proj_varlen(Tensor xn, Tensor W_qkvab, Tensor conv_w_qkv, int64_t H, int64_t dk, int64_t dv,
+                                   Tensor cu_seqlens, std::optional<Tensor> cache_q, std::optional<Tensor> cache_k,
+                                   std::optional<Tensor> cache_v, bool want_cache) {
+    check_bf16(xn, "xn");
+    check_bf16(W_qkvab, "W_qkvab");
+    check_bf16(conv_w_qkv, "conv_w_qkv");
+    TORCH_CHECK(xn.dim() == 2 || (xn.dim() == 3 && xn.size(0) == 1), "xn must be [T_total, D] or [1, T_total, D]");
+    const int64_t Ttot = xn.size(-2), D = xn.size(-1);
+    TORCH_CHECK(W_qkvab.dim() == 2 && W_qkvab.size(0) == 2 * H * dk + H * dv + 2 * H && W_qkvab.size(1) == D,
+                "W_qkvab must be [2 H dk + H dv + 2 H, D]");
+    TORCH_CHECK(conv_w_qkv.dim() == 2 && conv_w_qkv.size(0) == 2 * H * dk + H * dv, "conv_w_qkv must be [2 H dk + H dv, K]");
+    TORCH_CHECK(cu_seqlens.dim() == 1 && cu_seqlens.numel() >= 2, "cu_seqlens must be [N + 1]");
+    TORCH_CHECK(!cu_seqlens.is_cuda(), "in_proj_varlen takes host offsets (cu_seqlens on the CPU)");
+    const int64_t N = cu_seqlens.numel() - 1;
+    auto cu = cu_seqlens.to(at::kInt).contiguous();
+    const int64_t ck = conv_w_qkv.size(1);
+    const c10::DeviceGuard guard(xn.device());
+    auto o = xn.options();
+    auto q = at::empty({1, H, Ttot, dk}, o), k = at::empty({1, H, Ttot, dk}, o), v = at::empty({1, H, Ttot, dv}, o);
+    auto a = at::empty({1, H, Ttot}, o), b = at::empty({1, H, Ttot}, o);
+    std::vector<Tensor> res = {q, k, v, a, b};
+    gdn_bf16_t *cq = nullptr, *ckk = nullptr, *cv = nullptr;
+    if (want_cache) {
+        auto nq = at::empty({N, H * dk, ck - 1}, o), nk = at::empty({N, H * dk, ck - 1}, o),
+             nv = at::empty({N, H * dv, ck - 1}, o);
+        cq = bf_mut(nq);
+        ckk = bf_mut(nk);
+        cv = bf_mut(nv);
+        res.push_back(nq);
+        res.push_back(nk);
+        res.push_back(nv);
+    }
+    GDN_CHECK_STATUS(gdn_in_proj_varlen_hip(bf(xn), bf(W_qkvab), bf(conv_w_qkv), cu.data_ptr<int32_t>(), N,
+                                            opt_bf(cache_q, "cache_q", N * H * dk * (ck - 1)),
+                                            opt_bf(cache_k, "cache_k", N * H * dk * (ck - 1)),
+                                            opt_bf(cache_v, "cache_v", N * H * dv * (ck - 1)), cq, ckk, cv, bf_mut(q),
+                                            bf_mut(k), bf_mut(v), bf_mut(a), bf_mut(b), Ttot, D, H, dk, dv, ck,
+                                            stream_of(xn)),
+                     "in_proj_varlen");
+    return res;
+}
+
 // Decode conv step on P = xn W^T of one token; caches updated in place.
 std::vector<Tensor> decode_conv_step(Tensor P, Tensor conv_w_qkv, Tensor cache_q, Tensor cache_k, Tensor cache_v,
                                      int64_t H, int64_t dk, int64_t dv) {
@@ -384,10 +431,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            py::arg("token_major") = false);
     mp.def("prefill_varlen", &prefill_varlen,
            "Packed varlen prefill: q,k [1,H,Ttot,K] | v [1,H,Ttot,V] | a,b_logits [1,H,Ttot] | cu_seqlens [N+1] | "
-           "state_in [N,H,K,V] or empty.  Returns (out [1,H,Ttot,V] bf16, state_out [N,H,K,V] fp32)",
+           "state_in [N,H,K,V] or empty.  Returns (out [1,H,Ttot,V] bf16, or [1,Ttot,H,V] with token_major, "
+           "state_out [N,H,K,V] fp32)",
            py::arg("q"), py::arg("k"), py::arg("v"), py::arg("A_log"), py::arg("a"), py::arg("dt_bias"),
            py::arg("b_logits"), py::arg("cu_seqlens"), py::arg("state_in"), py::arg("scale"),
-           py::arg("mask") = py::none(), py::arg("max_seqlen") = 0);
+           py::arg("mask") = py::none(), py::arg("max_seqlen") = 0, py::arg("token_major") = false);
     // Reference attribute values; H and V are runtime parameters here (any H,
     // V % 16 == 0), K is 128 and the chunk is 64 as in the reference.
     mp.attr("H_DIM") = 16;
@@ -409,6 +457,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            py::arg("xn"), py::arg("W_qkvab"), py::arg("conv_w_qkv"), py::arg("H"), py::arg("dk"), py::arg("dv"),
            py::arg("cache_q") = py::none(), py::arg("cache_k") = py::none(), py::arg("cache_v") = py::none(),
            py::arg("want_cache") = false);
+    ml.def("in_proj_varlen", &in_proj_varlen,
+           "in_proj for packed sequences (host cu_seqlens): each sequence's conv starts from its own cache",
+           py::arg("xn"), py::arg("W_qkvab"), py::arg("conv_w_qkv"), py::arg("H"), py::arg("dk"), py::arg("dv"),
+           py::arg("cu_seqlens"), py::arg("cache_q") = py::none(), py::arg("cache_k") = py::none(),
+           py::arg("cache_v") = py::none(), py::arg("want_cache") = false);
     ml.def("decode_conv_step", &decode_conv_step, "Decode conv step with projected-token caches (in place)",
            py::arg("P"), py::arg("conv_w_qkv"), py::arg("cache_q"), py::arg("cache_k"), py::arg("cache_v"),
            py::arg("H"), py::arg("dk"), py::arg("dv"));

@@ -381,6 +381,96 @@ extern "C" int gdn_in_proj_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, 
     return gdn_proj::launch_proj(p, static_cast<hipStream_t>(stream));
 }
 
+namespace {
+__global__ void gdn_zero_u16_kernel(uint16_t* __restrict__ p, size_t n) {
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        p[i] = 0;
+}
+}  // namespace
+
+extern "C" int gdn_in_proj_varlen_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv,
+                                      const int32_t* cu_seqlens, int num_seqs, const gdn_bf16_t* cache_q_in,
+                                      const gdn_bf16_t* cache_k_in, const gdn_bf16_t* cache_v_in,
+                                      gdn_bf16_t* cache_q_out, gdn_bf16_t* cache_k_out, gdn_bf16_t* cache_v_out,
+                                      gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
+                                      int T_total, int D, int H, int dk, int dv, int conv_k, void* stream) {
+    using gdn_host::aligned;
+    using gdn_host::fail;
+    if (num_seqs < 0 || T_total < 0 || D <= 0 || H <= 0 || dk <= 0 || dv <= 0)
+        return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: num_seqs=%d T_total=%d D=%d H=%d dk=%d dv=%d", num_seqs,
+                    T_total, D, H, dk, dv);
+    if (D % 64 != 0) return fail(GDN_ERR_UNSUPPORTED, "in_proj_varlen: D=%d must be a multiple of 64", D);
+    if (conv_k < 1 || conv_k > 4)
+        return fail(GDN_ERR_UNSUPPORTED, "in_proj_varlen: conv_k=%d must be in 1..4", conv_k);
+    if (num_seqs == 0) return GDN_OK;
+    if (!cu_seqlens) return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: null cu_seqlens");
+    if (cu_seqlens[0] != 0 || cu_seqlens[num_seqs] != T_total)
+        return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: cu_seqlens must run from 0 to T_total=%d", T_total);
+    for (int i = 0; i < num_seqs; ++i)
+        if (cu_seqlens[i + 1] < cu_seqlens[i])
+            return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: cu_seqlens must be non-decreasing (at %d)", i);
+    if (T_total > 0 && (!xn || !W_qkvab || !conv_w_qkv || !q || !k || !v || !a || !b))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: null pointer argument");
+    if ((cache_q_out && (cache_q_out == cache_q_in)) || (cache_k_out && (cache_k_out == cache_k_in)) ||
+        (cache_v_out && (cache_v_out == cache_v_in)))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: conv caches in and out must not alias");
+    const int Hk = H * dk, Hv = H * dv, nc = conv_k - 1;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < num_seqs; ++i) {
+        const int t0 = cu_seqlens[i], len = cu_seqlens[i + 1] - t0;
+        auto cin = [&](const gdn_bf16_t* c, int width) {
+            return c ? c + static_cast<size_t>(i) * width * nc : nullptr;
+        };
+        auto cout = [&](gdn_bf16_t* c, int width) { return c ? c + static_cast<size_t>(i) * width * nc : nullptr; };
+        if (len == 0) {
+            // An empty sequence keeps its conv history (zeros without one).
+            const struct { const gdn_bf16_t* in; gdn_bf16_t* out; int width; } caches[3] = {
+                {cin(cache_q_in, Hk), cout(cache_q_out, Hk), Hk},
+                {cin(cache_k_in, Hk), cout(cache_k_out, Hk), Hk},
+                {cin(cache_v_in, Hv), cout(cache_v_out, Hv), Hv}};
+            for (const auto& c : caches) {
+                if (!c.out || nc == 0) continue;
+                const size_t bytes = static_cast<size_t>(c.width) * nc * 2;
+                if (c.in) {
+                    if (hipMemcpyAsync(c.out, c.in, bytes, hipMemcpyDeviceToDevice, st) != hipSuccess)
+                        return fail(GDN_ERR_HIP, "in_proj_varlen: cache copy failed");
+                } else {
+                    // a fill kernel, not a memset node, so the call stays safe to capture
+                    hipLaunchKernelGGL(gdn_zero_u16_kernel, dim3(64), dim3(256), 0, st, c.out, bytes / 2);
+                    const int rc = gdn_host::check_launch("gdn_zero_u16_kernel");
+                    if (rc != GDN_OK) return rc;
+                }
+            }
+            continue;
+        }
+        gdn_proj::ProjParams p = {};
+        p.x = xn + static_cast<size_t>(t0) * D;
+        if (!aligned(p.x, 16) || !aligned(W_qkvab, 16))
+            return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: xn/W need 16-byte alignment");
+        p.W = W_qkvab;
+        p.conv_w = conv_w_qkv;
+        p.B = 1;
+        p.T = len;
+        p.T_out = T_total;
+        p.D = D;
+        p.D_out = 2 * Hk + Hv + 2 * H;
+        p.conv_k = conv_k;
+        p.ngroups = 5;
+        p.groups[0] = gdn_proj::ProjGroup{0, Hk, dk, 1, 0, q + static_cast<size_t>(t0) * dk, cin(cache_q_in, Hk),
+                                          cout(cache_q_out, Hk)};
+        p.groups[1] = gdn_proj::ProjGroup{Hk, Hk, dk, 1, Hk, k + static_cast<size_t>(t0) * dk, cin(cache_k_in, Hk),
+                                          cout(cache_k_out, Hk)};
+        p.groups[2] = gdn_proj::ProjGroup{2 * Hk, Hv, dv, 1, 2 * Hk, v + static_cast<size_t>(t0) * dv,
+                                          cin(cache_v_in, Hv), cout(cache_v_out, Hv)};
+        p.groups[3] = gdn_proj::ProjGroup{2 * Hk + Hv, H, 1, 0, 0, a + t0, nullptr, nullptr};
+        p.groups[4] = gdn_proj::ProjGroup{2 * Hk + Hv + H, H, 1, 0, 0, b + t0, nullptr, nullptr};
+        const int rc = gdn_proj::launch_proj(p, st);
+        if (rc != GDN_OK) return rc;
+    }
+    return GDN_OK;
+}
+
 extern "C" int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q,
                                         gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, gdn_bf16_t* q, gdn_bf16_t* k,
                                         gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, int B, int H, int dk, int dv,

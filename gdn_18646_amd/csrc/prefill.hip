@@ -2203,11 +2203,15 @@ int gdn_prefill_noalloc_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_
                          dv, s.ptr, kScratchBytes, stream, 3);
 }
 
-int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
-                           const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
-                           const int32_t* cu_seqlens, int num_seqs, int max_seqlen, const float* state_in,
-                           float scale, gdn_bf16_t* out, float* state_out, int H, int T_total, int dk, int dv,
-                           void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int prefill_varlen(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                   const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                   const int32_t* cu_seqlens, int num_seqs, int max_seqlen, const float* state_in, float scale,
+                   gdn_bf16_t* out, float* state_out, int H, int T_total, int dk, int dv, void* workspace,
+                   size_t workspace_bytes, void* stream, int out_tm) {
     using gdn_host::aligned;
     using gdn_host::fail;
     int st = check_common("prefill_varlen", H, dk, dv);
@@ -2233,6 +2237,7 @@ int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_b
     p.out = out;
     p.state_out = state_out;
     p.cu = cu_seqlens;
+    p.out_tm = out_tm;
     p.dt_bias = dt_bias;
     p.scale = scale == 0.f ? 1.f / sqrtf(static_cast<float>(dk)) : scale;
     p.H = H;
@@ -2244,6 +2249,28 @@ int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_b
     const int nchunk_grid = (maxlen + kC - 1) / kC;
     const long long slots = static_cast<long long>(T_total) / kC + num_seqs + 1;
     return launch(p, num_seqs, nchunk_grid, false, workspace, workspace_bytes, slots, static_cast<hipStream_t>(stream), 3);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                           const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                           const int32_t* cu_seqlens, int num_seqs, int max_seqlen, const float* state_in,
+                           float scale, gdn_bf16_t* out, float* state_out, int H, int T_total, int dk, int dv,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    return prefill_varlen(q, k, v, A_log, a, dt_bias, b_logits, mask, cu_seqlens, num_seqs, max_seqlen, state_in,
+                          scale, out, state_out, H, T_total, dk, dv, workspace, workspace_bytes, stream, 0);
+}
+
+int gdn_prefill_varlen_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v, const float* A_log,
+                              const gdn_bf16_t* a, float dt_bias, const gdn_bf16_t* b_logits, const float* mask,
+                              const int32_t* cu_seqlens, int num_seqs, int max_seqlen, const float* state_in,
+                              float scale, gdn_bf16_t* out, float* state_out, int H, int T_total, int dk, int dv,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    return prefill_varlen(q, k, v, A_log, a, dt_bias, b_logits, mask, cu_seqlens, num_seqs, max_seqlen, state_in,
+                          scale, out, state_out, H, T_total, dk, dv, workspace, workspace_bytes, stream, 1);
 }
 
 }  // extern "C"

@@ -177,9 +177,9 @@ __global__ __launch_bounds__(256, 2) void gdn_proj_conv_kernel(gdn_proj::ProjPar
         size_t idx;
         if (grp.head_dim > 0) {
             const int hh = cc / grp.head_dim, dd = cc % grp.head_dim;
-            idx = ((static_cast<size_t>(b) * (grp.width / grp.head_dim) + hh) * p.T + t) * grp.head_dim + dd;
+            idx = ((static_cast<size_t>(b) * (grp.width / grp.head_dim) + hh) * p.T_out + t) * grp.head_dim + dd;
         } else {
-            idx = (static_cast<size_t>(b) * p.T + t) * grp.width + cc;
+            idx = (static_cast<size_t>(b) * p.T_out + t) * grp.width + cc;
         }
         grp.dst[idx] = f2bf_bits(y);
     }
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         // Element index of (b, t, column cc + i): b width T + t tstride + coff[i]
         // (token-major: tstride = width, coff = cc + i; head-major [B, width/hd,
         // T, hd]: tstride = hd, coff = ((cc + i) / hd) T hd + (cc + i) % hd).
-        const size_t seq = static_cast<size_t>(width) * p.T;
+        const size_t seq = static_cast<size_t>(width) * p.T_out;
         const int tstride = hd ? hd : width;
         const bool vec = hd == 0 || (hd & 3) == 0;  // the 4 columns are adjacent in memory
         size_t coff[4];
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             int h = hd ? cc / hd : 0, d = hd ? cc - h * hd : cc;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                coff[i] = hd ? static_cast<size_t>(h) * p.T * hd + d : static_cast<size_t>(cc + i);
+                coff[i] = hd ? static_cast<size_t>(h) * p.T_out * hd + d : static_cast<size_t>(cc + i);
                 if (hd && ++d == hd) {
                     d = 0;
                     ++h;
@@ -549,12 +549,17 @@ static bool mfma_path_ok(const ProjParams& p) {
     for (int g = 0; g < p.ngroups; ++g) {
         const ProjGroup& q = p.groups[g];
         if (q.col0 % 4 != 0 || q.width % 4 != 0 || q.cw_row0 % 4 != 0) return false;
-        if (!gdn_host::aligned(q.dst, 8)) return false;
+        // 8-byte stores where a lane's 4 columns are adjacent in memory;
+        // head_dim 1..3 (the layer's a/b) stores element by element.
+        const bool vec = q.head_dim == 0 || q.head_dim % 4 == 0;
+        if (!gdn_host::aligned(q.dst, vec ? 8 : 2)) return false;
     }
     return true;
 }
 
-int launch_proj(const ProjParams& p, hipStream_t stream) {
+int launch_proj(const ProjParams& pin, hipStream_t stream) {
+    ProjParams p = pin;
+    if (p.T_out < p.T) p.T_out = p.T;
     if (p.B == 0 || p.T == 0 || p.D_out == 0) return GDN_OK;
     if (mfma_path_ok(p)) {
         const int F3 = p.B * (p.T + kHalo);  // rows: kHalo cache rows + T tokens per sequence

@@ -33,6 +33,7 @@ struct ProjParams {
     const uint16_t* W;       // [D_out, D]
     const uint16_t* conv_w;  // [rows, conv_k]
     int B, T, D, D_out, conv_k;
+    int T_out;    // token stride of the outputs (>= T; 0 = T): a sequence written into a longer packed buffer
     int ngroups;  // groups sorted by col0, groups[0].col0 == 0
     ProjGroup groups[kMaxGroups];
 };

@@ -123,7 +123,7 @@ class GDNLayerCustom:
         return self.exts['rmsnorm'].forward(x2d.contiguous(), self.w['norm_gamma'], 1e-6, 256, 2)
 
     @torch.no_grad()
-    def forward(self, x, mask=None, return_state=False, state=None):
+    def forward(self, x, mask=None, return_state=False, state=None, cu_seqlens=None):
         """x [B, T, D] bf16 -> y [B, T, D] bf16.
 
         mask [B, T] fp32 (1 keep, 0 masked; default all ones).  With
@@ -131,9 +131,19 @@ class GDNLayerCustom:
         token (recurrent state and conv caches), so decode can continue the
         sequence.  ``state`` (optional) continues from an earlier state
         (initial recurrent state and conv caches).
+
+        ``cu_seqlens`` [N + 1] (host offsets: a list or CPU tensor) makes x
+        N packed sequences, x [1, T_total, D] (or [T_total, D]); every
+        sequence is its own prefill (its conv and state start from zero, or
+        from ``state``'s entry i), mask is [T_total] or [1, T_total], and the
+        returned state has one entry per sequence (recurrent [N, H, dk, dv],
+        conv caches [N, H d, K - 1], xn [N, K - 1, D]), which decode continues
+        as a batch of N.
         """
         if self.dt_bias_scalar is None:
             raise ValueError("prefill takes a scalar dt_bias (as the reference kernel)")
+        if cu_seqlens is not None:
+            return self._forward_packed(x, cu_seqlens, mask, return_state, state)
         B, T, _ = x.shape
         Dd, Hh, dk, dv = self.D, self.H, self.DK, self.DV
         if mask is None:  # empty = every token kept (no fill kernel)
@@ -156,6 +166,45 @@ class GDNLayerCustom:
         h = torch.cat([st.get('xn', torch.zeros(B, nc, Dd, dtype=x.dtype, device=x.device)), xn], 1)
         xn_hist = h[:, h.shape[1] - nc:]  # the last nc tokens ([:, -nc:] would keep all of them for nc = 0)
         return y, dict(recurrent=S, conv_q=outs[5], conv_k=outs[6], conv_v=outs[7], xn=xn_hist.contiguous())
+
+    def _forward_packed(self, x, cu_seqlens, mask, return_state, state):
+        Dd, Hh, dk, dv = self.D, self.H, self.DK, self.DV
+        cu = torch.as_tensor(cu_seqlens, dtype=torch.int32).cpu().contiguous()
+        N = cu.numel() - 1
+        Tt = x.shape[-2]
+        if x.shape[-1] != Dd or x.numel() != Tt * Dd:
+            raise ValueError(f"packed x must be [1, T_total, D] or [T_total, D], got {tuple(x.shape)}")
+        xn = self._rmsnorm(x.reshape(Tt, Dd))
+        st = state or {}
+        outs = self._layer.in_proj_varlen(xn, self.W_qkvab, self.conv_qkv, Hh, dk, dv, cu, st.get('conv_q'),
+                                          st.get('conv_k'), st.get('conv_v'), bool(return_state))
+        q, k, v, a, b = outs[:5]
+        s_in = st.get('recurrent')
+        if s_in is None:
+            s_in = torch.empty(0, dtype=torch.float32, device=x.device)
+        m = None if mask is None else mask.reshape(-1).float().contiguous()
+        # token-major output [1, T_total, H, dv]: feeds W_o without a transpose copy
+        o, S = self.exts['prefill'].prefill_varlen(q, k, v, self.A_log, a, self.dt_bias_scalar, b, cu, s_in,
+                                                   self.scale, mask=m, token_major=True)
+        y = (o.reshape(Tt, Hh * dv) @ self.W_o.T).reshape(x.shape)
+        if not return_state:
+            return y
+        # x_n history: the last K - 1 tokens of each sequence, earlier ones from
+        # the given state (zeros without one) where the sequence is shorter.
+        nc = self.CK - 1
+        prev = st.get('xn')
+        if prev is None:
+            prev = torch.zeros(N, nc, Dd, dtype=xn.dtype, device=x.device)
+        pool = torch.cat([prev.reshape(N * nc, Dd), xn], 0)
+        idx = []
+        for i in range(N):
+            lo, hi = int(cu[i]), int(cu[i + 1])
+            for j in range(nc):
+                t = hi - nc + j  # packed token index wanted
+                idx.append(N * nc + t if t >= lo else i * nc + nc - (lo - t))
+        hist = pool.index_select(0, torch.tensor(idx, dtype=torch.long, device=x.device)) if idx else \
+            pool.new_zeros(0, Dd)
+        return y, dict(recurrent=S, conv_q=outs[5], conv_k=outs[6], conv_v=outs[7], xn=hist.reshape(N, nc, Dd))
 
     @torch.no_grad()
     def decode(self, x, state=None, inplace=False):

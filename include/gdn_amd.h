@@ -20,6 +20,8 @@
  *                                kernels/rmsnorm.cu:112-131,251-276
  *   gdn_proj_conv_silu_hip    <- fused_proj_conv_silu, kernels/fused_proj_conv_silu.cu:298-355
  *   gdn_in_proj_hip           <- GDNLayerCustom.forward's projections, gdn_layer.py:240-252
+ *   gdn_in_proj_varlen_hip,   <- no reference counterpart (packed sequences through the layer;
+ *   gdn_prefill_varlen_tm_hip    the reference layer has no cu_seqlens path, gdn_layer.py:222-263)
  *   gdn_decode_conv_step_hip  <- _decode_conv_step / _decode_fused_proj_step, gdn_layer.py:43-69
  *   gdn_decode_in_proj_hip    <- GDNLayerCustom.decode's RMSNorm, projections and conv step,
  *                                gdn_layer.py:280-299 (with 43-69)
@@ -181,6 +183,20 @@ int gdn_prefill_varlen_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_b
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * gdn_prefill_varlen_hip with the output written token-major: out
+ * [T_total, H, dv] (the layout the output projection consumes); all else
+ * identical.  No reference counterpart (the layer's packed-sequence forward).
+ */
+int gdn_prefill_varlen_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                              const float* A_log, const gdn_bf16_t* a, float dt_bias,
+                              const gdn_bf16_t* b_logits, const float* mask,
+                              const int32_t* cu_seqlens, int num_seqs, int max_seqlen,
+                              const float* state_in, float scale,
+                              gdn_bf16_t* out, float* state_out,
+                              int H, int T_total, int dk, int dv,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * RMSNorm: y[r, :] = bf16(x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * gamma).
  *   x, y [R, D] bf16 (may not alias); gamma [D] bf16.  D % 8 == 0, D <= 16384.
  */
@@ -215,6 +231,25 @@ int gdn_in_proj_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, const gdn_b
                     gdn_bf16_t* cache_q_out, gdn_bf16_t* cache_k_out, gdn_bf16_t* cache_v_out,
                     gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
                     int B, int T, int D, int H, int dk, int dv, int conv_k, void* stream);
+
+/*
+ * gdn_in_proj_hip for num_seqs packed sequences: xn [T_total, D];
+ * cu_seqlens is a HOST int32 array [num_seqs + 1] (0 = cu[0] <= cu[1] <= ...
+ * <= cu[num_seqs] = T_total).  Each sequence's causal conv starts from its
+ * own cache (cache_*_in [num_seqs, H d, conv_k - 1], NULL = zeros) and
+ * cache_*_out [num_seqs, H d, conv_k - 1] (NULL = not written) receives its
+ * last conv_k - 1 projected tokens; outputs are packed head-major:
+ * q, k [H, T_total, dk]; v [H, T_total, dv]; a, b [H, T_total], as
+ * gdn_prefill_varlen_hip reads them.  One launch per non-empty sequence.
+ * No reference counterpart (the layer's packed-sequence forward; the
+ * reference layer has no cu_seqlens path, gdn_layer.py:222-263).
+ */
+int gdn_in_proj_varlen_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv,
+                           const int32_t* cu_seqlens, int num_seqs,
+                           const gdn_bf16_t* cache_q_in, const gdn_bf16_t* cache_k_in, const gdn_bf16_t* cache_v_in,
+                           gdn_bf16_t* cache_q_out, gdn_bf16_t* cache_k_out, gdn_bf16_t* cache_v_out,
+                           gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
+                           int T_total, int D, int H, int dk, int dv, int conv_k, void* stream);
 
 /*
  * Decode-step conv: P [B, 2 H dk + H dv + 2 H] bf16 holds xn W^T of the new
