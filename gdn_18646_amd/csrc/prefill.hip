@@ -1234,6 +1234,13 @@ __device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, i
 // One chunk of the state recurrence for this wave's 128 x 32 state tile, the
 // chunk's operands staged in `buf`; the output pass leaves the chunk's
 // outputs in the LDS tile `obuf` for the copy wave.
+// LDS reads run one phase ahead of the MFMAs that consume them: K S and
+// S^T Q^T go in four k-groups, each group's MFMAs issued after the next
+// group's fragment reads, and each later phase's operands (V and the gates,
+// Tp, K^T, Aq) are read while the phase before it computes.  Phase fences
+// (PHASE()) keep that order: the scheduler would otherwise sink reads to
+// their first use (exposing the LDS latency at every one) or hoist all of
+// them to the top (past the 256 VGPRs a wave has).
 template <int MODE>
 __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2], lds_u8* obuf, int wave, int lane,
                                             bool v_zero, uint32_t kt_lane) {
@@ -1242,66 +1249,70 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
     const int n = lane & 15, g = lane >> 4;
     const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + St::offG);
     const lds_u8* Vs = buf + St::offV + wave * 4 * kFragB;
+#define PHASE() __builtin_amdgcn_sched_barrier(0)
 
     // (a) X = K S and P^T = S^T Q^T.  The state's bf16 copy is the B operand
     //     of K S and the A operand of S^T Q^T as it stands (k = state rows
     //     32 s + 8 g + j in both).
-    // Phase fences (PHASE()) keep the scheduler from hoisting every fragment
-    // read of the step to its top: a wave then stays within the 256
-    // architectural VGPRs, and no accumulator round-trips through AGPRs each
-    // time the VALU touches it.
-#define PHASE() __builtin_amdgcn_sched_barrier(0)
-    const float gC = G[kC - 1];
+    bf16x8 kf[2][4], qf[2][OUT ? 4 : 1];
+    auto load_a = [&](int s, int slot) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            kf[slot][mt] = kfrag(buf + St::offK, 4 * mt + s, lane);
+            if constexpr (OUT) qf[slot][mt] = frag(buf, St::offQ + (4 * mt + s) * kFragB, lane);
+        }
+    };
+    i16x4 vv[2][4];
+    f32x4 gam[4], kd[4];
+    float gC = 0.f;
+    // (b)'s operands: V in the accumulator layout (column n, rows
+    // 16 mt + 4 g + i) -- source lane 4 j + a of group g of a transposing read
+    // fetches row 16 mt + 4 g + j, columns 16 nt + 4 a .. -- and the gates.
+    auto load_b = [&]() {
+        const lds_u8* vrow = Vs + ((4 * g + ((lane >> 2) & 3)) * 32 + 4 * (lane & 3)) * 2;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                vv[nt][mt] = v_zero ? i16x4{0, 0, 0, 0}
+                                    : __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                          (lds_i16x4*)(vrow + (16 * mt * 32 + 16 * nt) * 2));
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
+            kd[mt] = *reinterpret_cast<const lds_f32x4*>(G + 128 + 16 * mt + 4 * g);
+        }
+        gC = G[kC - 1];
+    };
     f32x4 X[4][2], P[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // In two k-halves, so the map pass holds half of the K fragments at a time.
+    load_a(0, 0);
+    PHASE();
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        bf16x8 kf[4][2], qf[OUT ? 4 : 1][2];
+    for (int s = 0; s < 4; ++s) {
+        if (s < 3)
+            load_a(s + 1, (s + 1) & 1);
+        else
+            load_b();
+        bf16x8 Bs[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const int f = 4 * mt + 2 * half + s2;
-                kf[mt][s2] = kfrag(buf + St::offK, f, lane);
-                if constexpr (OUT) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
+            for (int nt = 0; nt < 2; ++nt) {
+                X[mt][nt] = mfma16x16x32(kf[s & 1][mt], Bs[nt], X[mt][nt]);
+                if constexpr (OUT) P[mt][nt] = mfma16x16x32(Bs[nt], qf[s & 1][mt], P[mt][nt]);
             }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const int s = 2 * half + s2;
-            bf16x8 Bs[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
-                    X[mt][nt] = mfma16x16x32(kf[mt][s2], Bs[nt], X[mt][nt]);
-                    if constexpr (OUT) P[mt][nt] = mfma16x16x32(Bs[nt], qf[mt][s2], P[mt][nt]);
-                }
-        }
         PHASE();
     }
-    // (b) Y = V - gamma o X (in place in X).  V in the accumulator layout
-    //     (column n, rows 16 mt + 4 g + i): source lane 4 j + a of group g of
-    //     a transposing read fetches row 16 mt + 4 g + j, columns 16 nt + 4 a ..
-    i16x4 vv[2][4];
-    const lds_u8* vrow = Vs + ((4 * g + ((lane >> 2) & 3)) * 32 + 4 * (lane & 3)) * 2;
+    // (b) Y = V - gamma o X (in place in X), while Tp is read.
+    bf16x8 tf[6];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            vv[nt][mt] = v_zero ? i16x4{0, 0, 0, 0}
-                                : __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vrow + (16 * mt * 32 + 16 * nt) * 2));
-    f32x4 gam[4], kd[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
-        kd[mt] = *reinterpret_cast<const lds_f32x4*>(G + 128 + 16 * mt + 4 * g);
-    }
+    for (int i = 0; i < 6; ++i) tf[i] = frag(buf, St::offTp + i * kFragB, lane);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -1309,33 +1320,40 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 X[mt][nt][i] = bf2f(static_cast<uint16_t>(vv[nt][mt][i])) - gam[mt][i] * X[mt][nt][i];
-    // (c) dV = Tp Y (Tp lower triangular: six nonzero fragments).
-    bf16x8 tf[6];
+    bf16x8 BY[2][2];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) tf[i] = frag(buf, St::offTp + i * kFragB, lane);
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) BY[s][nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
+    PHASE();
+    // (c) dV = Tp Y (Tp lower triangular: six nonzero fragments), while the
+    //     first half of K^T is read.
+    bf16x8 ktf[8][2];
+    auto load_kt = [&](int r0) {
+#pragma unroll
+        for (int r = r0; r < r0 + 4; ++r) {
+            ktf[r][0] = ktfrag(buf + St::offK, kt_lane, r, 0);
+            ktf[r][1] = ktfrag(buf + St::offK, kt_lane, r, 1);
+        }
+    };
+    load_kt(0);
     f32x4 D[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        bf16x8 BY[2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) BY[nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int mt = 2 * s; mt < 4; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[nt], D[mt][nt]);
-    }
+            for (int nt = 0; nt < 2; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[s][nt], D[mt][nt]);
     PHASE();
-    // (d) S <- gamma_C S + K^T ((gamma_C / gamma) o dV).
-    bf16x8 ktf[8][2];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        ktf[r][0] = ktfrag(buf + St::offK, kt_lane, r, 0);
-        ktf[r][1] = ktfrag(buf + St::offK, kt_lane, r, 1);
-    }
+    // (d) S <- gamma_C S + K^T ((gamma_C / gamma) o dV) in two halves of
+    //     row tiles: the second half of K^T is read during the first, Aq
+    //     during the second.
+    bf16x8 af[OUT ? 6 : 1];
+    float co[4];
     bf16x8 BS0[2], BS1[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -1343,23 +1361,29 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
         BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
     }
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
+    for (int half = 0; half < 2; ++half) {
+        if (half == 0) {
+            load_kt(4);
+        } else if constexpr (OUT) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            S[r][nt] *= gC;
-            S[r][nt] = mfma16x16x32(ktf[r][0], BS0[nt], S[r][nt]);
-            S[r][nt] = mfma16x16x32(ktf[r][1], BS1[nt], S[r][nt]);
+            for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offAq + i * kFragB, lane);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) co[mt] = G[64 + 16 * mt + n];
         }
+#pragma unroll
+        for (int r = 4 * half; r < 4 * half + 4; ++r)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                S[r][nt] *= gC;
+                S[r][nt] = mfma16x16x32(ktf[r][0], BS0[nt], S[r][nt]);
+                S[r][nt] = mfma16x16x32(ktf[r][1], BS1[nt], S[r][nt]);
+            }
+        PHASE();
+    }
     // (e) O^T = (m scale gamma) o P^T + dV^T Aq^T: each lane holds 4
     //     consecutive output columns of token 16 mt + n, written to the
     //     output tile as 8 bytes.
     if constexpr (OUT) {
-        bf16x8 af[6];
-#pragma unroll
-        for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offAq + i * kFragB, lane);
-        float co[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) co[mt] = G[64 + 16 * mt + n];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const bf16x8 BD0 = pack8(D[0][nt], D[1][nt]), BD1 = pack8(D[2][nt], D[3][nt]);
