@@ -50,12 +50,17 @@ constexpr int kC = 64;    // chunk length
 constexpr int kDK = 128;  // key / query dim
 
 // Workspace record of one (chunk, head), written by the intra kernel and read
-// by the state kernels, in 1 KiB MFMA fragments (lane l's 16 bytes at 16 l):
-// the six nonzero fragments of Tp, the six of Aq, then the gate block.
+// by the state kernels, in 1 KiB MFMA fragments (lane l's 16 bytes at 16 l).
+// For the 16-column state kernel: the six nonzero fragments of Tp, the six of
+// Aq, the gate block.  The 32-column state kernel forms Aq itself and reads
+// the six of Tp, the gate block and the token block (log2 of the in-chunk
+// decay, m scale).  Gate block: gamma, m scale gamma, gamma_C / gamma.
 constexpr int kRecTp = 0;
 constexpr int kRecAq = 6;
-constexpr int kRecG = 12;
-constexpr int kRecFrags = 13;
+constexpr int kRecFull = 13;   // Tp, Aq, gates
+constexpr int kRecShort = 8;   // Tp, gates, tokens
+constexpr int kRecGShort = 6;  // gate block of the short record
+constexpr int kRecH = 7;       // token block of the short record
 
 struct PrefillParams {
     const uint16_t* q;
@@ -69,7 +74,8 @@ struct PrefillParams {
     uint16_t* out;
     float* state_out;
     const int32_t* cu;  // varlen offsets (nullable: batch mode)
-    u32x4* wsR;          // per (chunk, head) workspace records (kRecFrags 1 KiB fragments each)
+    u32x4* wsR;          // per (chunk, head) workspace records (rec_frags 1 KiB fragments each)
+    int intra_aq;        // the intra kernel forms Aq (kRecFull records, for the 16-column state kernel)
     float dt_bias;
     float scale;
     int H;
@@ -219,8 +225,9 @@ __device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUn
 // Tp fragments (mt, s) = (wave, 0), (wave, 1) of one record: fragments
 // (0, 1) and (1, 1) lie above the diagonal and are not stored; the others go
 // to slots (0,0) (1,0) (2,0) (2,1) (3,0) (3,1) in that order.
+template <int RF>
 __device__ __forceinline__ void store_tp(const PrefillParams& p, size_t wc, int wave, int lane, const u32x4 (&tpf)[2]) {
-    u32x4* rec = p.wsR + (wc * kRecFrags + kRecTp) * 64;
+    u32x4* rec = p.wsR + (wc * RF + kRecTp) * 64;
     if (wave < 2) {
         rec[wave * 64 + lane] = tpf[0];
     } else {
@@ -238,10 +245,15 @@ __device__ __forceinline__ void store_tp(const PrefillParams& p, size_t wc, int 
 // issued while stores are in flight waits for the stores as well (the vector
 // memory counter does not order reads against writes), so the next wait,
 // at the following unit's start, finds them long complete.
-// LDS use (about 47 KiB) allows three workgroups per CU, i.e. three waves
-// per SIMD: saying so lets the scheduler spend registers on hoisting loads.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gdn_prefill_intra_kernel(
-    PrefillParams p) {
+// AQ: also form the causal Aq (for the 16-column state kernel; the 32-column
+// one forms it itself).  LDS use (about 47 KiB with AQ, 39 KiB without)
+// allows three (four) workgroups per CU, i.e. three (four) waves per SIMD:
+// saying so lets the scheduler spend registers on hoisting loads.
+template <bool AQ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AQ ? 3 : 4, AQ ? 3 : 4))) void
+gdn_prefill_intra_kernel(PrefillParams p) {
+    constexpr int RF = AQ ? kRecFull : kRecShort;       // record length (fragments)
+    constexpr int RG = AQ ? kRecFull - 1 : kRecGShort;  // gate block
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -249,11 +261,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int g4 = lane >> 4;
 
     // The K tile is dead after step 3: step 5 keeps the fp32 T blocks there.
+    // Without AQ the bf16 Tp staging tile (Al) lives in the dead K tile too,
+    // after the fp32 T blocks.
+    constexpr int kTBytes = sizeof(float) * 6 * 16 * 20;
     __shared__ __attribute__((aligned(16))) bf16 Kl[kC][kKLD];
     __shared__ __attribute__((aligned(16))) float Ad[kC][kADS];
-    __shared__ __attribute__((aligned(16))) bf16 Al[kC][kBLD];
+    __shared__ __attribute__((aligned(16))) bf16 Al_own[AQ ? kC : 1][kBLD];
     __shared__ float s_lg2[kC], s_bm[kC], s_ms[kC];  // s_lg2: in-chunk log2 decay cumsum
-    static_assert(sizeof(Kl) >= sizeof(float) * 6 * 16 * 20, "the fp32 T blocks must fit in the K tile");
+    static_assert(sizeof(Kl) >= kTBytes + (AQ ? 0 : sizeof(bf16) * kC * kBLD), "the K tile must hold the T blocks");
+    bf16 (*const Al)[kBLD] =
+        AQ ? Al_own : reinterpret_cast<bf16 (*)[kBLD]>(reinterpret_cast<unsigned char*>(&Kl[0][0]) + kTBytes);
 
     int u = blockIdx.x;
     IntraUnit U = intra_unit(p, u);
@@ -288,19 +305,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     // needs block w (qa) and, for w < 2, block 3 (qb).  Rows are clamped to
     // the sequence; those rows get a zero output coefficient.
     bf16x8 qa[4], qb[4];
-    {
+    constexpr bool want_aq = AQ;
+    if constexpr (AQ) {
         const uint16_t* qr = p.q + (U.row_base + min(16 * wave + m16, nvalid - 1)) * kDK + 8 * g4;
 #pragma unroll
         for (int s = 0; s < 4; ++s) qa[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
-    if (wave < 2) {
+    if (AQ && wave < 2) {
         const uint16_t* qr = p.q + (U.row_base + min(48 + m16, nvalid - 1)) * kDK + 8 * g4;
 #pragma unroll
         for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
 
     // 2) Gates (wave 0, one token per lane) and the in-chunk log-cumsum.
-    float G0 = 0.f, G1 = 0.f, G2 = 0.f;  // this unit's G row, stored after step 3
+    float G0 = 0.f, G1 = 0.f, G2 = 0.f, H0 = 0.f, H1 = 0.f;  // this unit's gate and token rows, stored after step 3
     if (wave == 0) {
         const int t = lane;
         float lg = 0.f, bm = 0.f, m = 0.f;
@@ -314,6 +332,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         s_lg2[t] = s * 1.4426950408889634f;  // log2(e)
         s_bm[t] = bm;
         s_ms[t] = m * p.scale;
+        H0 = s * 1.4426950408889634f;
+        H1 = m * p.scale;
         const float gam = expf(s);
         G0 = gam;
         G1 = m * p.scale * gam;
@@ -330,7 +350,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         const int ti = t >> 2, tj = t & 3;  // tile (row ti, col tj)
         const int col = 16 * tj + m16;
         if (tj > ti) {
-            if (wave != 3) continue;
+            if (wave != 3 || !want_aq) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) Al[16 * ti + 4 * g4 + i][col] = f2bf(0.f);
             continue;
@@ -343,7 +363,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             const bf16x8 aK = *reinterpret_cast<const bf16x8*>(&Kl[16 * ti + m16][32 * s + 8 * g4]);
             const bf16x8 bK = *reinterpret_cast<const bf16x8*>(&Kl[16 * tj + m16][32 * s + 8 * g4]);
             accK = mfma16x16x32(aK, bK, accK);
-            accQ = mfma16x16x32(ti == wave ? qa[s] : qb[s], bK, accQ);
+            if constexpr (AQ) accQ = mfma16x16x32(ti == wave ? qa[s] : qb[s], bK, accQ);
         }
         const float lg2_col = s_lg2[col];
 #pragma unroll
@@ -351,7 +371,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             const int row = 16 * ti + 4 * g4 + i;
             const float d = __builtin_amdgcn_exp2f(s_lg2[row] - lg2_col);  // Gamma_{row,col}
             Ad[col][(row & 3) * kAQ + (row >> 2)] = row > col ? s_bm[row] * accK[i] * d : 0.f;
-            Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
+            if constexpr (AQ) Al[row][col] = f2bf(row >= col ? s_ms[row] * accQ[i] * d : 0.f);
         }
     }
     // vmcnt(0): nothing is in flight here (every Q load was consumed above),
@@ -363,23 +383,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     // then this unit's stores.
     if (N.valid) intra_load(p, N, tid, L);
     if (wave == 0) {
-        float* G = reinterpret_cast<float*>(p.wsR + (wc * kRecFrags + kRecG) * 64);
+        float* G = reinterpret_cast<float*>(p.wsR + (wc * RF + RG) * 64);
         G[lane] = G0;
         G[64 + lane] = G1;
         G[128 + lane] = G2;
+        if constexpr (!AQ) {
+            float* Hb = reinterpret_cast<float*>(p.wsR + (wc * RF + kRecH) * 64);
+            Hb[lane] = H0;
+            Hb[64 + lane] = H1;
+        }
     }
-    if (have_prev) store_tp(p, wc_prev, wave, lane, tpf);
+    if (have_prev) store_tp<RF>(p, wc_prev, wave, lane, tpf);
 
     // 4) The six nonzero Aq fragments (mt, s) = (0,0),(1,0),(2,0),(2,1),(3,0),(3,1):
     //    lane holds Aq[16mt + m][32s + pi(g, j)].
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-        if (i % 4 != wave) continue;
+        if (i % 4 != wave || !want_aq) continue;
         const int f = aq_slot(i), mt = f >> 1, s = f & 1;
         const bf16* rp = &Al[16 * mt + m16][32 * s + 4 * g4];
         const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16);
-        p.wsR[(wc * kRecFrags + kRecAq + i) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        p.wsR[(wc * RF + kRecAq + i) * 64 + lane] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
 
     // 5) T = (I + A)^-1 in fp32, blocked by 16 (block rows / columns I, J),
@@ -526,7 +551,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     u = u_next;
     U = N;
     }
-    if (have_prev) store_tp(p, wc_prev, wave, lane, tpf);
+    if (have_prev) store_tp<RF>(p, wc_prev, wave, lane, tpf);
 }
 
 // ---------------------------------------------------------------------------
@@ -619,9 +644,9 @@ struct Stager {
                 }
             } else {
                 // record fragments: Tp, then Aq (output only), then the gate block
-                const unsigned char* rec = reinterpret_cast<const unsigned char*>(p->wsR + wc * kRecFrags * 64);
+                const unsigned char* rec = reinterpret_cast<const unsigned char*>(p->wsR + wc * kRecFull * 64);
                 const int j = f - nK - nQ;
-                dma16(rec + (j < nT + nA ? j : kRecG) * kFragB, L->fr, dst);
+                dma16(rec + (j < nT + nA ? j : kRecFull - 1) * kFragB, L->fr, dst);
             }
         }
         if (v_on) {
@@ -1139,11 +1164,13 @@ struct Stage4 {
     static constexpr int offK = 0;
     static constexpr int offQ = 16 * kFragB;
     static constexpr int offR = offQ + (out ? 16 : 0) * kFragB;
-    static constexpr int nRec = out ? kRecFrags : 7;  // the map pass copies Tp and the gate block
+    // copied record fragments: Tp, the gate block and (output pass) the token block
+    static constexpr int nRec = out ? kRecShort : kRecGShort + 1;
     static constexpr int offTp = offR;
-    static constexpr int offAq = offR + kRecAq * kFragB;
-    static constexpr int offG = offR + (out ? kRecG : 6) * kFragB;
-    static constexpr int offV = offR + nRec * kFragB;
+    static constexpr int offG = offR + kRecGShort * kFragB;
+    static constexpr int offH = offR + kRecH * kFragB;
+    static constexpr int offAq = offR + nRec * kFragB;  // output pass: Aq, formed by the copy waves
+    static constexpr int offV = offAq + (out ? 6 : 0) * kFragB;
     static constexpr int bytes = offV + 16 * kFragB;
     static constexpr int ob_bytes = out ? kObBytes : 0;
     // waves: 4 compute, then (output pass) 2 copying chunks in and a store wave
@@ -1199,8 +1226,7 @@ __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf
     for (int i = 0; i < (St::nRec + STRIDE - 1) / STRIDE; ++i) {
         const int j = first + STRIDE * i;
         if (j < St::nRec) {
-            const int src = St::out ? j : (j < 6 ? j : kRecG);
-            dma16(rb + src * kFragB, L.r, buf + St::offR + j * kFragB);
+            dma16(rb + j * kFragB, L.r, buf + St::offR + j * kFragB);
         }
     }
     if (v_on) {  // job u: compute wave u / 4's columns, rows 16 (u % 4) ..
@@ -1219,10 +1245,72 @@ __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf
     }
 }
 
+// The output pass's copy wave `W` (of two) forms three of the six nonzero
+// fragments of the staged chunk's causal Aq = (m scale) (Q K^T o Gamma) into
+// the buffer's Aq area (wave 0: tiles (t, s) = (0,0) (1,0) (1,1) (2,0)
+// (2,1); wave 1: (2,2) (3,0) (3,1) (3,2) (3,3)), from the staged Q and K and
+// the token block.  Each tile is formed transposed, as K_s Q_t^T: its
+// accumulator (lane (n, g): s rows 4 g + i of token column n) is then,
+// packed, half of a fragment (mt, S) as the B operand of dV^T Aq^T reads it
+// (lane (n, g): token 16 mt + n, s in pi order).  Rows past a sequence's end
+// are clamped copies; their tokens have m scale = 0.
+template <int W>
+__device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
+    using St = Stage4<kModeOut>;
+    constexpr int NQ = W == 0 ? 3 : 2, q0 = W == 0 ? 0 : 2;  // Q tiles q0 ..
+    constexpr int NK = W == 0 ? 2 : 4;                       // K tiles 0 ..
+    const int n = lane & 15, g = lane >> 4;
+    const lds_f32* Hb = reinterpret_cast<const lds_f32*>(buf + St::offH);
+    bf16x8 qf[NQ][4], kf[NK][4];
+    float lt[NQ], mt[NQ];
+    f32x4 ls[NK];
+#pragma unroll
+    for (int t = 0; t < NQ; ++t) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) qf[t][kk] = frag(buf, St::offQ + (4 * (q0 + t) + kk) * kFragB, lane);
+        lt[t] = Hb[16 * (q0 + t) + n];
+        mt[t] = Hb[64 + 16 * (q0 + t) + n];
+    }
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) kf[t][kk] = kfrag(buf + St::offK, 4 * t + kk, lane);
+        ls[t] = *reinterpret_cast<const lds_f32x4*>(Hb + 16 * t + 4 * g);
+    }
+    auto tile = [&](int ti, int si) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = mfma16x16x32(kf[si][kk], qf[ti - q0][kk], acc);
+        f32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = mt[ti - q0] * acc[i] * __builtin_amdgcn_exp2f(lt[ti - q0] - ls[si][i]);
+            v[i] = (ti > si || 4 * g + i <= n) ? x : 0.f;
+        }
+        return pack4_bf16(v);
+    };
+    const u32x2 z = {0u, 0u};
+    auto put = [&](int slot, const u32x2 lo, const u32x2 hi) {
+        *reinterpret_cast<lds_u32x4*>(buf + St::offAq + slot * kFragB + 16 * lane) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    if constexpr (W == 0) {
+        put(0, tile(0, 0), z);
+        put(1, tile(1, 0), tile(1, 1));
+        put(2, tile(2, 0), tile(2, 1));
+    } else {
+        put(3, tile(2, 2), z);
+        put(4, tile(3, 0), tile(3, 1));
+        put(5, tile(3, 2), tile(3, 3));
+    }
+}
+
 // The copy wave: chunk c's output tile from LDS to `ob` (row 0, the
 // workgroup's first column), 4 rows of 256 bytes per instruction.
 template <bool FULL>
 __device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, int orow, int nvalid, int lane) {
+    // Opaque per call: otherwise the 16 per-lane row offsets are hoisted out
+    // of the chunk loop and held in registers that every wave then pays for.
+    asm volatile("" : "+s"(orow));
 #pragma unroll
     for (int i = 0; i < kC / 4; ++i) {
         const int row = 4 * i + (lane >> 4);
@@ -1241,9 +1329,9 @@ __device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, i
 // (PHASE()) keep that order: the scheduler would otherwise sink reads to
 // their first use (exposing the LDS latency at every one) or hoist all of
 // them to the top (past the 256 VGPRs a wave has).
-template <int MODE>
+template <int MODE, typename Mid>
 __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2], lds_u8* obuf, int wave, int lane,
-                                            bool v_zero, uint32_t kt_lane) {
+                                            bool v_zero, uint32_t kt_lane, Mid mid) {
     using St = Stage4<MODE>;
     constexpr bool OUT = St::out;
     const int n = lane & 15, g = lane >> 4;
@@ -1349,6 +1437,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[s][nt], D[mt][nt]);
     PHASE();
+    if constexpr (OUT) mid();  // the copy waves have formed Aq
     // (d) S <- gamma_C S + K^T ((gamma_C / gamma) o dV) in two halves of
     //     row tiles: the second half of K^T is read during the first, Aq
     //     during the second.
@@ -1470,12 +1559,69 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
                      static_cast<uint32_t>((lane >> 2) * dv * 2 + (lane & 3) * 16)};
     const uint32_t kt_lane = kt_lane_offset(lane);
 
+    const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
+    const int orow = p.out_tm ? p.H * dv : dv;
+    auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
+    auto obase = [&](int c) {  // out row of chunk c's first token, the workgroup's first column
+        const size_t tok = static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + static_cast<size_t>(c) * kC;
+        return p.out + (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + vg * 128;
+    };
+    auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
+    auto rec = [&](int c) { return p.wsR + (static_cast<size_t>(sq.slot0 + c) * p.H + h) * kRecShort * 64; };
+    auto issue = [&](int c, int bi) {
+        // Opaque per call: otherwise the copies' LDS addresses (buffer and
+        // fragment constants) are hoisted out of the chunk loop and held in
+        // SGPRs, which runs the kernel out of them.
+        int first = OUT ? wave - 4 : wave;
+        asm volatile("" : "+s"(first));
+        lds_u8* b = buf(bi);
+        constexpr int STRIDE = OUT ? St::loaders : 4;
+        if (nval(c) == kC)
+            stage4_issue<MODE, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
+        else
+            stage4_issue<MODE, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
+    };
+
+    // Chunk c = c_begin + k uses buffer k % 2 and output tile k % 2.  Barrier
+    // k opens step k: chunk c is staged, nobody reads buffer (k + 1) % 2 any
+    // more, and chunk c - 1's outputs are in tile (k - 1) % 2.  In the output
+    // pass a second barrier per step, before the compute waves' state update,
+    // publishes chunk c's Aq, which the two loading copy waves form after
+    // issuing chunk c + 1's copies.  The copy waves run their own loop (with
+    // the same barriers), so the compute waves' state is not live in it.
+    if constexpr (OUT) {
+        if (copier) {
+            if (loader && c_begin < c_end) issue(c_begin, 0);
+            for (int c = c_begin; c < c_end; ++c) {
+                const int k = c - c_begin;
+                if (loader) wait_vm<0>();  // chunk c staged
+                lds_barrier();
+                if (loader) {
+                    if (c + 1 < c_end) issue(c + 1, (k + 1) & 1);
+                    if (wave == 4)
+                        stage4_aq<0>(buf(k & 1), lane);
+                    else
+                        stage4_aq<1>(buf(k & 1), lane);
+                }
+                // Chunk c - 1 is never a sequence's partial last chunk here.
+                if (storer && k >= 1) stage4_store<true>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
+                lds_barrier();  // chunk c's Aq formed
+            }
+            lds_barrier();  // the last chunk's outputs are in LDS
+            if (storer && c_end > c_begin) {
+                const int c = c_end - 1, k = c - c_begin;
+                if (nval(c) == kC)
+                    stage4_store<true>(obuf(k & 1), obase(c), orow, kC, lane);
+                else
+                    stage4_store<false>(obuf(k & 1), obase(c), orow, nval(c), lane);
+            }
+            return;
+        }
+    }
+
     // State tile: S[r][nt][i] = S[rho(r, g, i)][col0_wave + 16 nt + n].
     f32x4 S[8][2];
-    if (copier) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) S[r][0] = S[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    } else if constexpr (MODE == kModeMap) {
+    if constexpr (MODE == kModeMap) {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
@@ -1506,55 +1652,17 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
             for (int nt = 0; nt < 2; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const size_t head_row0 = static_cast<size_t>(sq.b * p.H + h) * p.T_stride + sq.tok0;
-    const int orow = p.out_tm ? p.H * dv : dv;
-    auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
-    auto obase = [&](int c) {  // out row of chunk c's first token, the workgroup's first column
-        const size_t tok = static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + static_cast<size_t>(c) * kC;
-        return p.out + (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + vg * 128;
-    };
-    auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
-    auto rec = [&](int c) { return p.wsR + (static_cast<size_t>(sq.slot0 + c) * p.H + h) * kRecFrags * 64; };
-    auto issue = [&](int c, int bi) {
-        // Opaque per call: otherwise the copies' LDS addresses (buffer and
-        // fragment constants) are hoisted out of the chunk loop and held in
-        // SGPRs, which runs the kernel out of them.
-        int first = OUT ? wave - 4 : wave;
-        asm volatile("" : "+s"(first));
-        lds_u8* b = buf(bi);
-        constexpr int STRIDE = OUT ? St::loaders : 4;
-        if (nval(c) == kC)
-            stage4_issue<MODE, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
-        else
-            stage4_issue<MODE, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
-    };
-
-    // Chunk c = c_begin + k uses buffer k % 2 and output tile k % 2.  Barrier
-    // k opens step k: chunk c is staged, nobody reads buffer (k + 1) % 2 any
-    // more, and chunk c - 1's outputs are in tile (k - 1) % 2.
-    if (issuer && c_begin < c_end) issue(c_begin, 0);
+    if (!OUT && c_begin < c_end) issue(c_begin, 0);
     for (int c = c_begin; c < c_end; ++c) {
         const int k = c - c_begin;
-        if (issuer) wait_vm<0>();  // chunk c staged
+        if (!OUT) wait_vm<0>();  // chunk c staged (the map pass's compute waves copy)
         lds_barrier();
-        if (issuer && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
-        // Chunk c - 1 is never a sequence's partial last chunk here.
-        if (storer && k >= 1) stage4_store<true>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
-        if (!copier) state4_step<MODE>(buf(k & 1), S, obuf(k & 1), cw, lane, phi_cols, kt_lane);
+        if (!OUT && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
+        state4_step<MODE>(buf(k & 1), S, obuf(k & 1), cw, lane, phi_cols, kt_lane, [] { lds_barrier(); });
     }
 
     if constexpr (OUT) {
-        lds_barrier();  // the last chunk's outputs are in LDS
-        if (copier) {
-            if (storer && c_end > c_begin) {
-                const int c = c_end - 1, k = c - c_begin;
-                if (nval(c) == kC)
-                    stage4_store<true>(obuf(k & 1), obase(c), orow, kC, lane);
-                else
-                    stage4_store<false>(obuf(k & 1), obase(c), orow, nval(c), lane);
-            }
-            return;
-        }
+        lds_barrier();  // the last chunk's outputs are in LDS (matches the copy waves' final barrier)
         if (grp != ngroups - 1) return;
         float* so = p.state_out + static_cast<size_t>(sidx * p.H + h) * kDK * dv;
 #pragma unroll
@@ -1563,8 +1671,6 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
             for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n] = S[r][nt][i];
-    } else if (loader) {
-        return;
     } else if (phi_cols) {
         // phi as A fragments, transposed 16x16 tile by tile through this
         // wave's V area of buffer 0 (unused by identity columns): no copy is
@@ -1808,7 +1914,7 @@ __global__ void gdn_fill_zero_kernel(float* __restrict__ p, size_t n) {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-constexpr size_t kBytesRec = kRecFrags * 64 * 16;  // one (chunk, head) record
+constexpr size_t kFragBytes = 64 * 16;  // one record fragment
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -1884,6 +1990,9 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
     return s;
 }
 
+// Record length: the 32-column state kernel forms Aq itself.
+int rec_frags(const StatePlan& sp) { return sp.wide ? kRecShort : kRecFull; }
+
 struct WsLayout {
     size_t offR, offPsi, offPhi, offPlan, total;
 };
@@ -1899,7 +2008,7 @@ WsLayout ws_layout(long long slots, int H, long long nheads, int dv, const State
     const bool planned = planned_groups(sp, varlen);
     WsLayout L;
     L.offR = 0;
-    L.offPsi = align256(L.offR + ch * kBytesRec);
+    L.offPsi = align256(L.offR + ch * rec_frags(sp) * kFragBytes);
     const size_t units = planned      ? static_cast<size_t>(H) * plan_target(sp, H)
                          : sp.G > 1 ? static_cast<size_t>(nheads) * sp.G
                                     : 0;
@@ -1983,6 +2092,7 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
         return fail(GDN_ERR_INVALID_ARGUMENT, "prefill: workspace must be 256-byte aligned");
     char* ws = static_cast<char*>(workspace);
     p.wsR = reinterpret_cast<u32x4*>(ws + L.offR);
+    p.intra_aq = sp.wide ? 0 : 1;
 
     p.xcd_heads = (nheads % 8 == 0) ? 1 : 0;
     p.nchunk_grid = nchunk_grid;
@@ -1990,15 +2100,18 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
         const long long units = nheads * nchunk_grid;
         if (units > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
         p.intra_units = static_cast<int>(units);
-        // Persistent grid: three workgroups per CU (LDS-limited), a multiple
-        // of 8 so each workgroup's units stay on its XCD.
+        // Persistent grid: three or four workgroups per CU (LDS-limited), a
+        // multiple of 8 so each workgroup's units stay on its XCD.
         int dev = 0, ncu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
             ncu = 256;
-        long long nwg = std::min<long long>(units, 3LL * ncu);
+        long long nwg = std::min<long long>(units, (p.intra_aq ? 3LL : 4LL) * ncu);
         if (nwg >= 8) nwg &= ~7LL;
-        hipLaunchKernelGGL(gdn_prefill_intra_kernel, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p);
+        if (p.intra_aq)
+            hipLaunchKernelGGL(gdn_prefill_intra_kernel<true>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL(gdn_prefill_intra_kernel<false>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, stream, p);
         const int st = gdn_host::check_launch("gdn_prefill_intra_kernel");
         if (st != GDN_OK) return st;
     }

@@ -121,7 +121,8 @@ int gdn_prefill_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_
  * process ends; the call allocates nothing.  A shape whose
  * gdn_prefill_workspace_bytes() exceeds that size is refused with
  * GDN_ERR_WORKSPACE before any HIP call (e.g. B=1, H=16, T=8192, dk=dv=128
- * needs 54 MiB and fits; B=4, H=16, T=4096 needs 84 MiB and does not).
+ * needs 40 MiB and B=4, H=16, T=4096 56 MiB, which fit; B=4, H=16, T=8192
+ * needs 88 MiB and does not).
  * All calls on one GPU share the buffer: calls that overlap on one GPU (two
  * streams, two threads) race, so serialise them.  Nothing in it needs to
  * start zeroed.  Outputs are bit-identical to gdn_prefill_hip's.

@@ -37,19 +37,22 @@ def test_host_functions():
     assert lib.gdn_abi_version() == 1
     assert lib.gdn_status_string(0) == b"ok"
     assert lib.gdn_status_string(3) == b"workspace too small"
-    # 13 KiB per (chunk, head): the nonzero Tp and Aq fragments (6 KiB each), gate block
-    # (1 KiB); the metric shape has 128 chunks x 16 heads.  With only 16 (sequence, head)
-    # pairs the state pass splits each sequence into 16 chunk groups, each with a 128 x dv
-    # fp32 zero-state result and a 128 x 128 bf16 transition.
+    # dv a multiple of 128: 8 KiB per (chunk, head), the six nonzero Tp fragments, the
+    # gate block and the token block (1 KiB each); the metric shape has 128 chunks x 16
+    # heads.  With only 16 (sequence, head) pairs the state pass splits each sequence into
+    # 16 chunk groups, each with a 128 x dv fp32 zero-state result and a 128 x 128 bf16
+    # transition.
     b = lib.gdn_prefill_workspace_bytes(1, 16, 8192, 128, 128)
-    per_chunk = 2048 * (6 + 6 + 1) * 1024
+    per_chunk = 2048 * (6 + 1 + 1) * 1024
     groups = 16 * 16 * (128 * 128 * 4 + 128 * 128 * 2)
     assert per_chunk + groups <= b < per_chunk + groups + 8192
     # enough (sequence, head) pairs to fill the chip: no groups
     b = lib.gdn_prefill_workspace_bytes(16, 16, 8192, 128, 128)
     assert 16 * per_chunk <= b < 16 * per_chunk + 8192
     assert lib.gdn_prefill_workspace_bytes(1, 16, 0, 128, 128) == 0
+    # other dv: 13 KiB records, the six Aq fragments in place of the token block
     assert lib.gdn_prefill_varlen_workspace_bytes(3, 2, 130, 128, 64) >= (130 // 64 + 3) * 2 * 13 * 1024
+    assert lib.gdn_prefill_workspace_bytes(1, 2, 640, 128, 64) >= 10 * 2 * 13 * 1024
 
 
 FAKE = 4096  # non-null, 16-byte aligned; validation fails before it is ever dereferenced
@@ -59,7 +62,7 @@ def test_prefill_noalloc_refuses_oversized_shape():
     """The static scratch limit is checked before any HIP call (none runs here)."""
     with pytest.raises(GdnError, match="WORKSPACE.*static buffer"):
         abi.call("gdn_prefill_noalloc_hip", *([FAKE] * 5), 0.0, FAKE, FAKE, None, 0.0, FAKE, FAKE,
-                 4, 16, 4096, 128, 128, None)
+                 4, 16, 8192, 128, 128, None)
     with pytest.raises(GdnError, match="UNSUPPORTED.*dk=64"):
         abi.call("gdn_prefill_noalloc_hip", *([FAKE] * 5), 0.0, FAKE, FAKE, None, 0.0, FAKE, FAKE,
                  1, 16, 64, 64, 128, None)
