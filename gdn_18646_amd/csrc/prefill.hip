@@ -1173,9 +1173,10 @@ struct Stage4 {
     static constexpr int offV = offAq + (out ? 6 : 0) * kFragB;
     static constexpr int bytes = offV + 16 * kFragB;
     static constexpr int ob_bytes = out ? kObBytes : 0;
-    // waves: 4 compute, then (output pass) 2 copying chunks in and a store wave
+    // waves: 4 compute, then (output pass) 2 copying chunks in, a store wave
+    // and the Aq wave
     static constexpr int loaders = out ? 2 : 0;
-    static constexpr int nWaves = 4 + loaders + (out ? 1 : 0);
+    static constexpr int nWaves = 4 + loaders + (out ? 2 : 0);
     static constexpr int nStores = out ? kC * 256 / kFragB : 0;  // output store instructions per chunk
 };
 
@@ -1245,46 +1246,40 @@ __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf
     }
 }
 
-// The output pass's copy wave `W` (of two) forms three of the six nonzero
-// fragments of the staged chunk's causal Aq = (m scale) (Q K^T o Gamma) into
-// the buffer's Aq area (wave 0: tiles (t, s) = (0,0) (1,0) (1,1) (2,0)
-// (2,1); wave 1: (2,2) (3,0) (3,1) (3,2) (3,3)), from the staged Q and K and
-// the token block.  Each tile is formed transposed, as K_s Q_t^T: its
-// accumulator (lane (n, g): s rows 4 g + i of token column n) is then,
-// packed, half of a fragment (mt, S) as the B operand of dV^T Aq^T reads it
-// (lane (n, g): token 16 mt + n, s in pi order).  Rows past a sequence's end
-// are clamped copies; their tokens have m scale = 0.
-template <int W>
+// The output pass's Aq wave forms the six nonzero fragments of the staged
+// chunk's causal Aq = (m scale) (Q K^T o Gamma) into the buffer's Aq area,
+// from the staged Q and K and the token block.  Each 16x16 tile (t, s) is
+// formed transposed, as K_s Q_t^T: its accumulator (lane (n, g): s rows
+// 4 g + i of token column n) is then, packed, half of a fragment (mt, S) as
+// the B operand of dV^T Aq^T reads it (lane (n, g): token 16 mt + n, s in
+// pi order).  Rows past a sequence's end are clamped copies; their tokens
+// have m scale = 0.
 __device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
     using St = Stage4<kModeOut>;
-    constexpr int NQ = W == 0 ? 3 : 2, q0 = W == 0 ? 0 : 2;  // Q tiles q0 ..
-    constexpr int NK = W == 0 ? 2 : 4;                       // K tiles 0 ..
     const int n = lane & 15, g = lane >> 4;
     const lds_f32* Hb = reinterpret_cast<const lds_f32*>(buf + St::offH);
-    bf16x8 qf[NQ][4], kf[NK][4];
-    float lt[NQ], mt[NQ];
-    f32x4 ls[NK];
+    bf16x8 qf[4][4], kf[4][4];
+    float lt[4], mt[4];
+    f32x4 ls[4];
 #pragma unroll
-    for (int t = 0; t < NQ; ++t) {
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) qf[t][kk] = frag(buf, St::offQ + (4 * (q0 + t) + kk) * kFragB, lane);
-        lt[t] = Hb[16 * (q0 + t) + n];
-        mt[t] = Hb[64 + 16 * (q0 + t) + n];
-    }
-#pragma unroll
-    for (int t = 0; t < NK; ++t) {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) kf[t][kk] = kfrag(buf + St::offK, 4 * t + kk, lane);
+        for (int kk = 0; kk < 4; ++kk) {
+            qf[t][kk] = frag(buf, St::offQ + (4 * t + kk) * kFragB, lane);
+            kf[t][kk] = kfrag(buf + St::offK, 4 * t + kk, lane);
+        }
+        lt[t] = Hb[16 * t + n];
+        mt[t] = Hb[64 + 16 * t + n];
         ls[t] = *reinterpret_cast<const lds_f32x4*>(Hb + 16 * t + 4 * g);
     }
     auto tile = [&](int ti, int si) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) acc = mfma16x16x32(kf[si][kk], qf[ti - q0][kk], acc);
+        for (int kk = 0; kk < 4; ++kk) acc = mfma16x16x32(kf[si][kk], qf[ti][kk], acc);
         f32x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float x = mt[ti - q0] * acc[i] * __builtin_amdgcn_exp2f(lt[ti - q0] - ls[si][i]);
+            const float x = mt[ti] * acc[i] * __builtin_amdgcn_exp2f(lt[ti] - ls[si][i]);
             v[i] = (ti > si || 4 * g + i <= n) ? x : 0.f;
         }
         return pack4_bf16(v);
@@ -1293,15 +1288,12 @@ __device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
     auto put = [&](int slot, const u32x2 lo, const u32x2 hi) {
         *reinterpret_cast<lds_u32x4*>(buf + St::offAq + slot * kFragB + 16 * lane) = u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
-    if constexpr (W == 0) {
-        put(0, tile(0, 0), z);
-        put(1, tile(1, 0), tile(1, 1));
-        put(2, tile(2, 0), tile(2, 1));
-    } else {
-        put(3, tile(2, 2), z);
-        put(4, tile(3, 0), tile(3, 1));
-        put(5, tile(3, 2), tile(3, 3));
-    }
+    put(0, tile(0, 0), z);
+    put(1, tile(1, 0), tile(1, 1));
+    put(2, tile(2, 0), tile(2, 1));
+    put(3, tile(2, 2), z);
+    put(4, tile(3, 0), tile(3, 1));
+    put(5, tile(3, 2), tile(3, 3));
 }
 
 // The copy wave: chunk c's output tile from LDS to `ob` (row 0, the
@@ -1437,7 +1429,6 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[s][nt], D[mt][nt]);
     PHASE();
-    if constexpr (OUT) mid();  // the copy waves have formed Aq
     // (d) S <- gamma_C S + K^T ((gamma_C / gamma) o dV) in two halves of
     //     row tiles: the second half of K^T is read during the first, Aq
     //     during the second.
@@ -1454,6 +1445,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
         if (half == 0) {
             load_kt(4);
         } else if constexpr (OUT) {
+            mid();  // the Aq wave has formed Aq
 #pragma unroll
             for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offAq + i * kFragB, lane);
 #pragma unroll
@@ -1539,11 +1531,13 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
     const SeqInfo sq = seq_info(p, sidx);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Copy waves (output pass): 4 and 5 copy chunk c + 1 in, 6 writes chunk
-    // c - 1's outputs.  In the map pass the compute waves copy (`issuer`).
+    // c - 1's outputs, 7 forms chunk c's Aq.  In the map pass the compute
+    // waves copy (`issuer`).
     const bool loader = OUT && wave >= 4 && wave < 4 + St::loaders;
     const bool storer = OUT && wave == 4 + St::loaders;
+    const bool aqw = OUT && wave == 5 + St::loaders;
     const bool issuer = OUT ? loader : true;
-    const bool copier = loader || storer;
+    const bool copier = loader || storer || aqw;
     const int cw = copier ? 0 : wave;  // compute wave (column block)
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
@@ -1585,10 +1579,10 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
     // Chunk c = c_begin + k uses buffer k % 2 and output tile k % 2.  Barrier
     // k opens step k: chunk c is staged, nobody reads buffer (k + 1) % 2 any
     // more, and chunk c - 1's outputs are in tile (k - 1) % 2.  In the output
-    // pass a second barrier per step, before the compute waves' state update,
-    // publishes chunk c's Aq, which the two loading copy waves form after
-    // issuing chunk c + 1's copies.  The copy waves run their own loop (with
-    // the same barriers), so the compute waves' state is not live in it.
+    // pass a second barrier per step, in the middle of the compute waves'
+    // state update, publishes chunk c's Aq, formed meanwhile by the Aq wave.
+    // The copy waves run their own loop (with the same barriers), so the
+    // compute waves' state is not live in it.
     if constexpr (OUT) {
         if (copier) {
             if (loader && c_begin < c_end) issue(c_begin, 0);
@@ -1596,13 +1590,8 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
                 const int k = c - c_begin;
                 if (loader) wait_vm<0>();  // chunk c staged
                 lds_barrier();
-                if (loader) {
-                    if (c + 1 < c_end) issue(c + 1, (k + 1) & 1);
-                    if (wave == 4)
-                        stage4_aq<0>(buf(k & 1), lane);
-                    else
-                        stage4_aq<1>(buf(k & 1), lane);
-                }
+                if (loader && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
+                if (aqw) stage4_aq(buf(k & 1), lane);
                 // Chunk c - 1 is never a sequence's partial last chunk here.
                 if (storer && k >= 1) stage4_store<true>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
                 lds_barrier();  // chunk c's Aq formed
