@@ -45,6 +45,7 @@ SIGNATURES = {
     "gdn_decode_conv_step_hip": (_I, [_P] * 10 + [_I] * 5 + [_P]),
     "gdn_decode_in_proj_hip": (_I, [_P, _P, _F] + [_P] * 11 + [_I] * 6 + [_P]),
     "gdn_decode_out_proj_hip": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "gdn_layer_decode_step_hip": (_I, [_P, _P, _F] + [_P] * 10 + [_F] + [_P] * 8 + [_I] * 6 + [_P]),
 }
 
 STATUS = {0: "GDN_OK", 1: "GDN_ERR_INVALID_ARGUMENT", 2: "GDN_ERR_UNSUPPORTED",

@@ -414,6 +414,48 @@ Tensor decode_out_proj(Tensor o, Tensor W) {
     return y;
 }
 
+// One whole decode step (in place on the caches, the x_n history and S):
+// x [B, D] -> y [B, D] bf16; q..o are caller-owned scratch.
+void decode_step(Tensor x, Tensor gamma, double eps, Tensor W_qkvab, Tensor conv_w_qkv, Tensor cache_q,
+                 Tensor cache_k, Tensor cache_v, std::optional<Tensor> xn_hist, Tensor A_log, Tensor dt_bias,
+                 Tensor S_in, Tensor S_out, double scale, Tensor W_o, Tensor q, Tensor k, Tensor v, Tensor a, Tensor b,
+                 Tensor o, Tensor y, int64_t H, int64_t dk, int64_t dv) {
+    for (const Tensor* t : {&x, &gamma, &W_qkvab, &conv_w_qkv, &cache_q, &cache_k, &cache_v, &W_o, &q, &k, &v, &a, &b, &y})
+        check_bf16(*t, "decode_step bf16 argument");
+    for (const Tensor* t : {&A_log, &dt_bias, &S_in, &S_out, &o}) check_f32(*t, "decode_step fp32 argument");
+    TORCH_CHECK(x.dim() == 2, "x must be [B, D]");
+    const int64_t B = x.size(0), D = x.size(1);
+    const int64_t ck = conv_w_qkv.size(1);
+    TORCH_CHECK(W_qkvab.dim() == 2 && W_qkvab.size(0) == 2 * H * dk + H * dv + 2 * H && W_qkvab.size(1) == D,
+                "W_qkvab must be [2 H dk + H dv + 2 H, D]");
+    TORCH_CHECK(conv_w_qkv.dim() == 2 && conv_w_qkv.size(0) == 2 * H * dk + H * dv, "conv_w_qkv must be [2 H dk + H dv, K]");
+    TORCH_CHECK(gamma.numel() == D, "gamma must have D entries");
+    TORCH_CHECK(cache_q.numel() == B * H * dk * (ck - 1) && cache_k.numel() == B * H * dk * (ck - 1) &&
+                    cache_v.numel() == B * H * dv * (ck - 1),
+                "conv caches must be [B, H d, K - 1]");
+    TORCH_CHECK(A_log.numel() == H && dt_bias.numel() == H, "A_log, dt_bias must be [H]");
+    TORCH_CHECK(S_in.numel() == B * H * dk * dv && S_out.numel() == B * H * dk * dv, "S must be [B, H, dk, dv]");
+    TORCH_CHECK(W_o.dim() == 2 && W_o.size(0) == D && W_o.size(1) == H * dv, "W_o must be [D, H dv]");
+    TORCH_CHECK(q.numel() == B * H * dk && k.numel() == B * H * dk && v.numel() == B * H * dv && a.numel() == B * H &&
+                    b.numel() == B * H && o.numel() == B * H * dv && y.numel() == B * D,
+                "scratch q, k [B, H dk], v [B, H dv], a, b [B, H], o [B, H dv] fp32, y [B, D]");
+    gdn_bf16_t* hist = nullptr;
+    if (xn_hist.has_value() && xn_hist->defined() && xn_hist->numel() > 0) {
+        check_bf16(*xn_hist, "xn_hist");
+        TORCH_CHECK(xn_hist->numel() == B * (ck - 1) * D, "xn_hist must be [B, K - 1, D]");
+        hist = bf_mut(*xn_hist);
+    }
+    const c10::DeviceGuard guard(x.device());
+    GDN_CHECK_STATUS(gdn_layer_decode_step_hip(bf(x), bf(gamma), static_cast<float>(eps), bf(W_qkvab), bf(conv_w_qkv),
+                                               bf_mut(cache_q), bf_mut(cache_k), bf_mut(cache_v), hist,
+                                               A_log.data_ptr<float>(), dt_bias.data_ptr<float>(),
+                                               S_in.data_ptr<float>(), S_out.data_ptr<float>(),
+                                               static_cast<float>(scale), bf(W_o), bf_mut(q), bf_mut(k), bf_mut(v),
+                                               bf_mut(a), bf_mut(b), o.data_ptr<float>(), bf_mut(y), B, D, H, dk, dv,
+                                               ck, stream_of(x)),
+                     "decode_step");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -472,6 +514,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            py::arg("H"), py::arg("dk"), py::arg("dv"));
     ml.def("decode_out_proj", &decode_out_proj, "Decode step output projection (B <= 16): bf16(o) W^T",
            py::arg("o"), py::arg("W"));
+    ml.def("decode_step", &decode_step,
+           "Whole decode step (B <= 16): in-projection, recurrence, out-projection in one call; caches, xn_hist "
+           "and S_out updated in place, y written; q, k, v, a, b, o are scratch",
+           py::arg("x"), py::arg("gamma"), py::arg("eps"), py::arg("W_qkvab"), py::arg("conv_w_qkv"),
+           py::arg("cache_q"), py::arg("cache_k"), py::arg("cache_v"), py::arg("xn_hist"), py::arg("A_log"),
+           py::arg("dt_bias"), py::arg("S_in"), py::arg("S_out"), py::arg("scale"), py::arg("W_o"), py::arg("q"),
+           py::arg("k"), py::arg("v"), py::arg("a"), py::arg("b"), py::arg("o"), py::arg("y"), py::arg("H"),
+           py::arg("dk"), py::arg("dv"));
 
     auto mj = m.def_submodule("proj", "Projection + causal conv + SiLU");
     mj.def("forward", &proj_forward, "Fused linear projection + causal depthwise conv1d + SiLU (bf16)",

@@ -71,6 +71,16 @@ __device__ __forceinline__ float sum8(float v) {
     v += dpp_f<0x141>(v);  // row_half_mirror
     return v;
 }
+// Sum over the whole wave, the same in every lane: sum8, the row mirror
+// (lane i <-> 15-i of each 16-lane row) for the row sums, then the four row
+// sums read into scalars and added in row order.  No LDS round trips.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = sum8(v);
+    v += dpp_f<0x140>(v);  // row_mirror
+    const int b = __float_as_int(v);
+    return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+           (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
 
 // MFMA 16x16x32 bf16 -> fp32.  Operand layout used throughout (the k order
 // inside a lane is free as long as A and B agree on it):

@@ -112,14 +112,15 @@ struct SkinnyParams {
 // tail, then gamma (MAXSTEPS * 512 bytes).
 __host__ __device__ inline size_t skinny_x_bytes(int B, int K) { return (static_cast<size_t>(B) * K * 2 + 1023) / 1024 * 1024; }
 
-// A uniform value the optimiser cannot trace back to its kernel-argument load:
-// a select between such loads would otherwise become one vector load from the
-// argument block at a lane-selected offset, whose wait also waits for every
-// weight load in flight.
-template <typename T>
-__device__ __forceinline__ T opaque_sgpr(T v) {
-    asm("" : "+s"(v));
-    return v;
+// The output group (q, k, v, a, b) of the workgroup's columns, as a uniform
+// value.  The host guarantees that the q, k and v widths are multiples of the
+// workgroup's column count, so only the a and b columns can share a
+// workgroup; those take group 3 here and pick a or b per lane.  Selecting
+// group descriptors with a uniform index keeps them in scalar registers
+// (a per-lane select between kernel arguments becomes a vector load from the
+// argument block, and its wait also waits for every weight load in flight).
+__device__ __forceinline__ int skinny_wg_group(const SkinnyParams& p, int n0) {
+    return n0 >= p.col0[3] ? 3 : n0 >= p.col0[2] ? 2 : n0 >= p.col0[1] ? 1 : 0;
 }
 
 // MODE 0: in-projection, MODE 1: out-projection.  Wave w takes the 32-wide
@@ -168,6 +169,55 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
         }
     }
 
+    bf16x8 af[MAXSTEPS];
+    const int er = tid >> 4, ec = tid & 15, en = n0 + ec;
+    const bool eown = tid < kSkM * kSkMaxCols && er < p.B && ec < p.cols && en < p.N;
+    int egi = 0;
+    uint16_t* ecache = nullptr;
+    const int nc = p.conv_k - 1, sh = 4 - p.conv_k;
+    // in-projection epilogue inputs, raw bf16 (converted where used, after
+    // the products, so no wait for them lands before the weight loads issue):
+    // kEpiLoads loads, all unconditional
+    constexpr int kEpiLoads = 9;
+    uint16_t rt0 = 0, rt1 = 0, rt2 = 0, rt3 = 0, ru0 = 0, ru1 = 0, ru2 = 0;
+    u32x4 hold1 = {0u, 0u, 0u, 0u}, hold2 = {0u, 0u, 0u, 0u};
+    const int hstep = blockIdx.x;
+    const bool hown = MODE == 0 && p.xn_hist && nc > 0 && hstep < ksteps && wave == hstep % kSkWaves;
+    uint16_t* const hrow = p.xn_hist + static_cast<size_t>(arow_ld) * nc * p.K + 32 * hstep + 8 * g4;
+    if constexpr (MODE == 0) {
+        // Epilogue ownership: thread t < 256 computes output (row t / 16,
+        // column n0 + t % 16).  Its conv taps and cache window load first
+        // (from clamped, valid positions; small loads issued behind the
+        // weight loads would wait for a queue full of them), right-aligned in
+        // four slots: slot 3 = the new token, slots 0..2 = the cached tokens,
+        // oldest first; slots before 4 - conv_k hold zero weight and input.
+        const int er_ld = min(er, p.B - 1), en_ld = min(en, p.N - 1);
+        const int wgi = __builtin_amdgcn_readfirstlane(skinny_wg_group(p, n0));
+        egi = wgi < 3 ? wgi : (en_ld >= p.col0[4] ? 4 : 3);
+        const int cgi = wgi < 3 ? wgi : 0;  // a/b columns read column 0's entries, unused
+        const int ccol = wgi < 3 ? en_ld : 0;
+        const uint16_t* wrow = p.conv_w + static_cast<size_t>(ccol) * p.conv_k;
+        uint16_t* const cbase = cgi == 0 ? p.cache[0] : cgi == 1 ? p.cache[1] : p.cache[2];
+        const int cwidth = cgi == 0 ? p.width[0] : cgi == 1 ? p.width[1] : p.width[2];
+        const int ccol0 = cgi == 0 ? p.col0[0] : cgi == 1 ? p.col0[1] : p.col0[2];
+        ecache = cbase + (static_cast<size_t>(er_ld) * cwidth + (ccol - ccol0)) * nc;
+        const uint16_t* cread = nc > 0 ? ecache : wrow;  // conv_k == 1: no cache
+        rt0 = wrow[max(0 - sh, 0)];
+        rt1 = wrow[max(1 - sh, 0)];
+        rt2 = wrow[max(2 - sh, 0)];
+        rt3 = wrow[3 - sh];
+        ru0 = cread[max(0 - sh, 0)];
+        ru1 = cread[max(1 - sh, 0)];
+        ru2 = cread[max(2 - sh, 0)];
+        // x_n history: workgroup b shifts and appends K step b (wave b % 8,
+        // slot b / 8); the grid has at least K / 32 workgroups (extra ones own
+        // no columns).  The entries it moves load now (unconditionally, from
+        // x where there is nothing to move: a conditional load would merge
+        // registers across a branch and wait).
+        hold1 = *reinterpret_cast<const u32x4*>(hown && nc > 1 ? hrow + p.K : p.x);
+        hold2 = *reinterpret_cast<const u32x4*>(hown && nc > 2 ? hrow + 2 * p.K : p.x);
+    }
+
     // Weight rows n0 + lane % 16 (B operand): one buffer load per step slot
     // (rows past N and slots past the last step read zeros).
     const auto wrs = buffer_rsrc(p.W + static_cast<size_t>(min(n0, p.N)) * p.K,
@@ -177,22 +227,16 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
 #pragma unroll
     for (int s = 0; s < MAXSTEPS; ++s) bw[s] = buffer_load16(wrs, s < nsteps ? wvoff : kPast, 2 * kSkStride * s);
 
-    bf16x8 af[MAXSTEPS];
-    const int er = tid >> 4, ec = tid & 15, en = n0 + ec;
-    const bool eown = tid < kSkM * kSkMaxCols && er < p.B && ec < p.cols && en < p.N;
-    int egi = 0;
-    float ws0 = 0.f, ws1 = 0.f, ws2 = 0.f, ws3 = 0.f, cs0 = 0.f, cs1 = 0.f, cs2 = 0.f;
-    uint16_t* ecache = nullptr;
-    const int nc = p.conv_k - 1, sh = 4 - p.conv_k;
     if constexpr (MODE == 0) {
-        // The DMA completes before the MAXSTEPS weight loads issued after it.
-        // Barriers here order LDS only: a full __syncthreads() fence would
-        // also wait for the weight loads in flight.
-        wait_vm<MAXSTEPS>();
+        // The DMA has landed (the kEpiLoads epilogue loads and the MAXSTEPS
+        // weight loads issued after it may still be in flight).  Barriers
+        // here order LDS only: a full __syncthreads() fence would also wait
+        // for the loads.
+        wait_vm<MAXSTEPS + kEpiLoads>();
         lds_barrier();
         // RMSNorm statistics in gdn_rmsnorm_kernel's order (a lane sums its
-        // 16-byte chunks lane + 64 u, then a butterfly over the wave), so x_n
-        // equals that kernel's output bit for bit.
+        // 16-byte chunks lane + 64 u, then wave_sum_dpp), so x_n equals that
+        // kernel's output bit for bit.
         for (int m = wave; m < p.B; m += kSkWaves) {
             float ss = 0.f;
             for (int c = lane; c < p.K / 8; c += 64) {
@@ -201,49 +245,9 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            ss = wave_sum_dpp(ss);
             if (lane == 0) s_inv[m] = 1.f / sqrtf(ss / static_cast<float>(p.K) + p.eps);
         }
-
-        // Epilogue ownership: thread t < 256 computes output (row t / 16,
-        // column n0 + t % 16).  Its conv taps and cache window load now (from
-        // clamped, valid positions), right-aligned in four slots: slot 3 = the
-        // new token, slots 0..2 = the cached tokens, oldest first; slots before
-        // 4 - conv_k hold zero weight and zero input.
-        const int er_ld = min(er, p.B - 1), en_ld = min(en, p.N - 1);
-#pragma unroll
-        for (int q = 1; q < 5; ++q)
-            if (en_ld >= p.col0[q]) egi = q;
-        const int cgi = egi < 3 ? egi : 0;  // a/b columns read column 0's entries, unused
-        const int ccol = egi < 3 ? en_ld : 0;
-        const uint16_t* wrow = p.conv_w + static_cast<size_t>(ccol) * p.conv_k;
-        uint16_t* const cbase = cgi == 0 ? opaque_sgpr(p.cache[0]) : cgi == 1 ? opaque_sgpr(p.cache[1]) : opaque_sgpr(p.cache[2]);
-        const int cwidth = cgi == 0 ? opaque_sgpr(p.width[0]) : cgi == 1 ? opaque_sgpr(p.width[1]) : opaque_sgpr(p.width[2]);
-        const int ccol0 = cgi == 0 ? opaque_sgpr(p.col0[0]) : cgi == 1 ? opaque_sgpr(p.col0[1]) : opaque_sgpr(p.col0[2]);
-        ecache = cbase + (static_cast<size_t>(er_ld) * cwidth + (ccol - ccol0)) * nc;
-        const uint16_t* cread = nc > 0 ? ecache : wrow;  // conv_k == 1: no cache
-        const float t0 = bf2f(wrow[max(0 - sh, 0)]), t1 = bf2f(wrow[max(1 - sh, 0)]);
-        const float t2 = bf2f(wrow[max(2 - sh, 0)]), t3 = bf2f(wrow[3 - sh]);
-        const float u0 = bf2f(cread[max(0 - sh, 0)]), u1 = bf2f(cread[max(1 - sh, 0)]);
-        const float u2 = bf2f(cread[max(2 - sh, 0)]);
-        ws0 = sh <= 0 ? t0 : 0.f;
-        ws1 = sh <= 1 ? t1 : 0.f;
-        ws2 = sh <= 2 ? t2 : 0.f;
-        ws3 = t3;
-        cs0 = sh <= 0 ? u0 : 0.f;
-        cs1 = sh <= 1 ? u1 : 0.f;
-        cs2 = sh <= 2 ? u2 : 0.f;
-        // x_n history: workgroup b shifts and appends K step b (wave b % 8,
-        // slot b / 8); the grid has at least K / 32 workgroups (extra ones own
-        // no columns).  The entries it moves load now.
-        const int hstep = blockIdx.x;
-        const bool hown = p.xn_hist && nc > 0 && hstep < ksteps && wave == hstep % kSkWaves;
-        uint16_t* const hrow = p.xn_hist + static_cast<size_t>(arow_ld) * nc * p.K + 32 * hstep + 8 * g4;
-        // (unconditional loads, from x where there is nothing to move: a
-        // conditional one would merge registers across a branch and wait)
-        const u32x4 hold1 = *reinterpret_cast<const u32x4*>(hown && nc > 1 ? hrow + p.K : p.x);
-        const u32x4 hold2 = *reinterpret_cast<const u32x4*>(hown && nc > 2 ? hrow + 2 * p.K : p.x);
         lds_barrier();
 
         // A operand x_n = bf16((x * inv) * gamma), as gdn_rmsnorm_kernel.
@@ -296,6 +300,10 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
     } else {
         float y = P;
         if (egi < 3) {
+            const float ws0 = sh <= 0 ? bf2f(rt0) : 0.f, ws1 = sh <= 1 ? bf2f(rt1) : 0.f;
+            const float ws2 = sh <= 2 ? bf2f(rt2) : 0.f, ws3 = bf2f(rt3);
+            const float cs0 = sh <= 0 ? bf2f(ru0) : 0.f, cs1 = sh <= 1 ? bf2f(ru1) : 0.f;
+            const float cs2 = sh <= 2 ? bf2f(ru2) : 0.f;
             float sc = ws3 * P;
             sc += ws0 * cs0;
             sc += ws1 * cs1;
@@ -310,15 +318,16 @@ void gdn_decode_skinny_kernel(SkinnyParams p) {
             if (nc > 0) ecache[nc - 1] = f2bf_bits(P);
             y = silu_f(sc);
         }
-        uint16_t* dbase = opaque_sgpr(p.dst[0]);
-        int dw = opaque_sgpr(p.width[0]), dc = opaque_sgpr(p.col0[0]);
-#pragma unroll
-        for (int q = 1; q < 5; ++q)
-            if (egi == q) {
-                dbase = opaque_sgpr(p.dst[q]);
-                dw = opaque_sgpr(p.width[q]);
-                dc = opaque_sgpr(p.col0[q]);
-            }
+        // uniform selects, then the per-lane a / b choice between two scalars
+        const int wgi = __builtin_amdgcn_readfirstlane(skinny_wg_group(p, n0));
+        uint16_t* dbase = wgi == 0 ? p.dst[0] : wgi == 1 ? p.dst[1] : wgi == 2 ? p.dst[2] : p.dst[3];
+        int dw = wgi == 0 ? p.width[0] : wgi == 1 ? p.width[1] : wgi == 2 ? p.width[2] : p.width[3];
+        int dc = wgi == 0 ? p.col0[0] : wgi == 1 ? p.col0[1] : wgi == 2 ? p.col0[2] : p.col0[3];
+        if (egi == 4) {
+            dbase = p.dst[4];
+            dw = p.width[4];
+            dc = p.col0[4];
+        }
         dbase[static_cast<size_t>(er) * dw + (en - dc)] = f2bf_bits(y);
     }
 }
@@ -524,6 +533,8 @@ extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gam
         return fail(GDN_ERR_UNSUPPORTED, "decode_in_proj: D=%d must be a multiple of 32, at most %d", D,
                     kSkStride * 16);
     if (conv_k < 1 || conv_k > 4) return fail(GDN_ERR_UNSUPPORTED, "decode_in_proj: conv_k=%d must be in 1..4", conv_k);
+    if ((H * dk) % 16 != 0 || (H * dv) % 16 != 0)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_in_proj: H dk=%d and H dv=%d must be multiples of 16", H * dk, H * dv);
     if (B == 0) return GDN_OK;
     if (!x || !gamma || !W_qkvab || !conv_w_qkv || !q || !k || !v || !a || !b ||
         (conv_k > 1 && (!cache_q || !cache_k || !cache_v)))
@@ -577,4 +588,21 @@ extern "C" int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W_o, gd
     p.o = o;
     p.y = y;
     return launch_skinny<1>(p, static_cast<hipStream_t>(stream), "gdn_decode_skinny_kernel<out>");
+}
+
+extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps,
+                                         const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q,
+                                         gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, gdn_bf16_t* xn_hist,
+                                         const float* A_log, const float* dt_bias, const float* S_in, float* S_out,
+                                         float scale, const gdn_bf16_t* W_o, gdn_bf16_t* q, gdn_bf16_t* k,
+                                         gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, float* o, gdn_bf16_t* y, int B,
+                                         int D, int H, int dk, int dv, int conv_k, void* stream) {
+    // The three launches validate their own arguments; the first failure
+    // returns before anything later is launched.
+    int st = gdn_decode_in_proj_hip(x, gamma, eps, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v,
+                                    a, b, B, D, H, dk, dv, conv_k, stream);
+    if (st != GDN_OK) return st;
+    st = gdn_decode_hip(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, S_out, B, H, dk, dv, stream);
+    if (st != GDN_OK) return st;
+    return gdn_decode_out_proj_hip(o, W_o, y, B, H * dv, D, stream);
 }

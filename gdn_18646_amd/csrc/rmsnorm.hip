@@ -12,11 +12,6 @@ namespace {
 
 using namespace gdn;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 template <int CHUNKS>  // 16-byte chunks per lane
 __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __restrict__ x,
@@ -38,7 +33,7 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __rest
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
     }
-    const float inv = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+    const float inv = 1.f / sqrtf(wave_sum_dpp(ss) / static_cast<float>(D) + eps);
     const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
     u32x4* yr = reinterpret_cast<u32x4*>(y + static_cast<size_t>(row) * D);
 #pragma unroll

@@ -12,8 +12,10 @@ Pipeline per call (all GPU, one stream):
            (and, on request, the conv cache for decode) -> chunked prefill
            (output written token-major) -> W_o GEMM.  No .item() host sync: dt_bias is read once at
            construction (call ``refresh()`` after changing the weights).
-  decode   RMSNorm kernel -> xn W^T GEMM -> decode conv step over the cached
-           projections -> decode kernel (state update in place when asked)
+  decode   one host call per step (B <= 16): the fused RMSNorm + q/k/v/a/b
+           projection + conv step kernel, the decode kernel (state update in
+           place when asked) and the W_o projection kernel.  Larger batches:
+           RMSNorm kernel -> xn W^T GEMM -> decode conv step -> decode kernel
            -> W_o GEMM.
 
 The baseline (pure PyTorch) layer of the reference is the oracle's
@@ -99,6 +101,7 @@ class GDNLayerCustom:
         self.D, self.H, self.DK, self.DV, self.CK = dims(weights)
         self.scale = self.DK ** -0.5
         self.chunk = int(self.exts['prefill'].C_DIM)
+        self._scratch = {}
         self.refresh()
 
     def refresh(self):
@@ -118,6 +121,19 @@ class GDNLayerCustom:
 
     def init_decode_state(self, B, device=None):
         return _zero_decode_state(self.w, B, device=device)
+
+    def _decode_scratch(self, B, device):
+        """Per-(B, device) intermediates of the fused decode step, kept across steps."""
+        key = (B, str(device))
+        buf = self._scratch.get(key)
+        if buf is None:
+            bf = dict(dtype=torch.bfloat16, device=device)
+            Hh, dk, dv = self.H, self.DK, self.DV
+            buf = (torch.empty(B, Hh, dk, **bf), torch.empty(B, Hh, dk, **bf), torch.empty(B, Hh, dv, **bf),
+                   torch.empty(B, Hh, **bf), torch.empty(B, Hh, **bf),
+                   torch.empty(B, Hh, dv, dtype=torch.float32, device=device))
+            self._scratch[key] = buf
+        return buf
 
     def _rmsnorm(self, x2d):
         return self.exts['rmsnorm'].forward(x2d.contiguous(), self.w['norm_gamma'], 1e-6, 256, 2)
@@ -227,25 +243,29 @@ class GDNLayerCustom:
             S_out = torch.empty_like(state['recurrent'])
         fused = self.fused_decode and B <= 16
         if fused:
-            # RMSNorm, projection, conv step and the x_n history in one launch
+            # The whole step in one host call: RMSNorm + projections + conv
+            # step + x_n history, the recurrence, the output projection.
             xn_hist = state['xn'] if inplace else state['xn'].clone()
-            q, k, v, a, b = self._layer.decode_in_proj(x.reshape(B, Dd).contiguous(), self.gamma, 1e-6,
-                                                       self.W_qkvab, self.conv_qkv, cq, ck, cv, xn_hist,
-                                                       Hh, dk, dv)
-        else:
-            xn = self._rmsnorm(x.reshape(B, Dd))
-            P = xn @ self.W_qkvab.T
-            q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv)
-            xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
+            q, k, v, a, b, o = self._decode_scratch(B, x.device)
+            y = torch.empty(B, 1, Dd, dtype=torch.bfloat16, device=x.device)
+            self._layer.decode_step(x.reshape(B, Dd).contiguous(), self.gamma, 1e-6, self.W_qkvab, self.conv_qkv,
+                                    cq, ck, cv, xn_hist, self.A_log, self.dt_bias_vec, state['recurrent'], S_out,
+                                    self.scale, self.W_o, q, k, v, a, b, o, y.view(B, Dd), Hh, dk, dv)
             if inplace:
-                state['xn'].copy_(xn_hist)  # same tensor, so a captured step stays valid
+                return y, state
+            return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist)
+        # Shapes the fused step does not take (B > 16, wide D): library GEMMs
+        # around the conv-step and decode kernels.
+        xn = self._rmsnorm(x.reshape(B, Dd))
+        P = xn @ self.W_qkvab.T
+        q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv)
+        xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
+        if inplace:
+            state['xn'].copy_(xn_hist)  # same tensor, so a captured step stays valid
         o = torch.empty(B, Hh, dv, dtype=torch.float32, device=x.device)
         self.exts['decode'].forward(q, k, v, a, b, self.A_log, self.dt_bias_vec, state['recurrent'], self.scale,
                                     o, S_out)
-        if fused:
-            y = self._layer.decode_out_proj(o.reshape(B, Hh * dv), self.W_o).reshape(B, 1, Dd)
-        else:
-            y = o.to(x.dtype).reshape(B, 1, Hh * dv) @ self.W_o.T
+        y = o.to(x.dtype).reshape(B, 1, Hh * dv) @ self.W_o.T
         if inplace:
             return y, state
         return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist.contiguous())

@@ -26,6 +26,7 @@
  *   gdn_decode_in_proj_hip    <- GDNLayerCustom.decode's RMSNorm, projections and conv step,
  *                                gdn_layer.py:280-299 (with 43-69)
  *   gdn_decode_out_proj_hip   <- GDNLayerCustom.decode's output projection, gdn_layer.py:309
+ *   gdn_layer_decode_step_hip <- GDNLayerCustom.decode as a whole, gdn_layer.py:265-316
  */
 #ifndef GDN_AMD_H
 #define GDN_AMD_H
@@ -291,6 +292,23 @@ int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float e
  */
 int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W, gdn_bf16_t* y, int B, int K, int N,
                             void* stream);
+
+/*
+ * One whole decode step of the layer, on `stream`: gdn_decode_in_proj_hip
+ * (RMSNorm, projections, conv step, x_n history), gdn_decode_hip (state S,
+ * in place when S_out == S_in) and gdn_decode_out_proj_hip, so a serving loop
+ * pays one host call per step.  q, k, v, a, b ([B, H dk] x2, [B, H dv],
+ * [B, H] x2 bf16) and o ([B, H dv] fp32) are caller-owned scratch; y is
+ * [B, D] bf16.  Constraints and errors are those of the three entry points
+ * (the first failure returns before anything later is launched).
+ * Replaces GDNLayerCustom.decode (gdn_layer.py:265-316) as a whole.
+ */
+int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps, const gdn_bf16_t* W_qkvab,
+                              const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q, gdn_bf16_t* cache_k,
+                              gdn_bf16_t* cache_v, gdn_bf16_t* xn_hist, const float* A_log, const float* dt_bias,
+                              const float* S_in, float* S_out, float scale, const gdn_bf16_t* W_o, gdn_bf16_t* q,
+                              gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, float* o, gdn_bf16_t* y,
+                              int B, int D, int H, int dk, int dv, int conv_k, void* stream);
 
 #ifdef __cplusplus
 }

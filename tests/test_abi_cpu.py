@@ -126,6 +126,16 @@ def test_decode_projection_validation_errors():
         abi.call("gdn_decode_out_proj_hip", FAKE + 4, FAKE, FAKE, 4, 2048, 2048, None)
 
 
+def test_decode_step_validation_errors():
+    """The fused step checks each stage's arguments before that stage launches."""
+    step_args = lambda B, D, dv: ([FAKE, FAKE, 1e-6] + [FAKE] * 10 + [0.1] + [FAKE] * 8 + [B, D, 2, 128, dv, 4, None])
+    with pytest.raises(GdnError, match="decode_in_proj.*B=17"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(17, 2048, 128))
+    with pytest.raises(GdnError, match="decode_in_proj.*D=100"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(4, 100, 128))
+    abi.call("gdn_layer_decode_step_hip", *step_args(0, 2048, 128))  # B == 0: no-op
+
+
 def test_binding_module_api_matches_reference():
     """Module names, attrs and signatures of the reference's pybind modules."""
     exts = compile_kernels()
