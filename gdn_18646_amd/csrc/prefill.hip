@@ -1919,7 +1919,8 @@ struct StatePlan {
 // `exact`: max_chunks is the exact chunk count of every sequence, so the
 // group count is trimmed until no group is empty.  Workspace sizing uses the
 // untrimmed count, which never decreases as sequences grow.
-StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact) {
+// `varlen`: packed sequences of unequal lengths.
+StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact, bool varlen) {
     StatePlan s;
     s.wide = dv % 128 == 0;
     if (s.wide) {
@@ -1927,9 +1928,15 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact)
         s.NW_out = s.NW_map = 4;
         s.nvg_out = dv / 128;
         s.nvg_map = (dv + kDK) / 128;
+        // Chunk groups when the output pass alone would leave CUs idle: below
+        // 256 output workgroups for packed sequences (groups also balance
+        // their unequal lengths), below 128 for equal lengths (measured at
+        // T = 8192: 128 (sequence, head) pairs run 1.2x faster as one group
+        // each than as two, where the map pass and scan cost more than the
+        // idle half of the chip).
         const long long base = nheads * s.nvg_out;  // output-pass workgroups (one per CU) with one group
         long long G = 1;
-        if (base < 256 && max_chunks >= 8)
+        if (base < (varlen ? 256 : 128) && max_chunks >= 8)
             G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
         if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
         s.G = G < 2 ? 1 : static_cast<int>(G);
@@ -2072,7 +2079,7 @@ int launch(PrefillParams& p, int nseq, int nchunk_grid, bool exact, void* worksp
            long long slots, hipStream_t stream, int phases) {
     using gdn_host::fail;
     const long long nheads = static_cast<long long>(nseq) * p.H;
-    const StatePlan sp = plan_state(nheads, p.dv, nchunk_grid, exact);
+    const StatePlan sp = plan_state(nheads, p.dv, nchunk_grid, exact, p.cu != nullptr);
     const bool varlen = p.cu != nullptr;
     const WsLayout L = ws_layout(slots, p.H, nheads, p.dv, sp, varlen, nseq);
     if (!workspace || ws_bytes < L.total)
@@ -2165,7 +2172,7 @@ size_t gdn_prefill_workspace_bytes(int B, int H, int T, int dk, int dv) {
     const long long nch = (T + kC - 1) / kC;
     const long long slots = static_cast<long long>(B) * nch;
     const long long nheads = static_cast<long long>(B) * H;
-    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, nch, false), false, B).total;
+    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, nch, false, false), false, B).total;
 }
 
 size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int dk, int dv) {
@@ -2175,7 +2182,7 @@ size_t gdn_prefill_varlen_workspace_bytes(int num_seqs, int H, int T_total, int 
     const long long nheads = static_cast<long long>(num_seqs) * H;
     // Whether chunk groups are used only grows with the longest sequence: size
     // for T_total (the per-sequence plan then fits in H x 256 / (H nvg) maps).
-    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, (T_total + kC - 1) / kC, false), true, num_seqs)
+    return ws_layout(slots, H, nheads, dv, plan_state(nheads, dv, (T_total + kC - 1) / kC, false, true), true, num_seqs)
         .total;
 }
 

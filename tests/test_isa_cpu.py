@@ -1,12 +1,13 @@
 """ISA checks of the decode-step in-projection (gdn_decode_skinny_kernel<0, *>)
 in gdn_18646_amd/csrc/layer.hip, on the CPU (hipcc cross-compiles gfx950).
 
-The kernel copies x and gamma to LDS with global_load_lds, then issues its
-MAXSTEPS weight loads, then waits with vmcnt(MAXSTEPS): vector memory
+The kernel copies x and gamma to LDS with global_load_lds, then issues the
+epilogue's EPI small loads (conv taps, cache window, x_n history) and its
+MAXSTEPS weight loads, then waits with vmcnt(MAXSTEPS + EPI): vector memory
 operations retire in issue order, so that wait covers the LDS copies only if
-exactly MAXSTEPS vector memory operations sit between the last copy and the
-wait.  A compiler that moved another load (or a spill) into that window would
-let RMSNorm read LDS before the copy lands; this test fails first.
+exactly MAXSTEPS + EPI vector memory operations sit between the last copy and
+the wait.  A compiler that moved another load (or a spill) into that window
+would let RMSNorm read LDS before the copy lands; this test fails first.
 """
 
 import os
@@ -47,6 +48,9 @@ def test_in_proj_dma_wait_covers_only_the_weight_loads(layer_asm, maxsteps):
     wait = next(i for i in range(last_dma, len(body)) if re.search(r"s_waitcnt vmcnt\(\d+\)", body[i]))
     n = int(re.search(r"vmcnt\((\d+)\)", body[wait]).group(1))
     between = [ln.strip() for ln in body[last_dma + 1:wait] if VMEM.match(ln)]
-    assert n == maxsteps, f"first wait after the copies is vmcnt({n}), expected vmcnt({maxsteps})"
-    assert len(between) == maxsteps and all(ln.startswith("buffer_load_dwordx4") for ln in between), between
+    epi = 9  # kEpiLoads in layer.hip: 7 global_load_ushort + 2 global_load_dwordx4
+    assert n == maxsteps + epi, f"first wait after the copies is vmcnt({n}), expected vmcnt({maxsteps + epi})"
+    assert len(between) == maxsteps + epi, between
+    assert sum(ln.startswith("buffer_load_dwordx4") for ln in between) == maxsteps, between
+    assert all(ln.startswith(("buffer_load_dwordx4", "global_load_ushort", "global_load_dwordx4")) for ln in between)
     assert not any("scratch_" in ln for ln in body), "the kernel spills"
