@@ -327,6 +327,45 @@ def main():
             f"parity {leg.get('parity')}")
         del dl, gl_, ov, Sv
 
+    # ------------------------------------------------------------------ decode (config 1)
+    if "decode" in legs:
+        d1 = synth.decode_inputs(1, 4, K, V, seed=0)
+        g1 = {k: v.to(dev) for k, v in d1.items()}
+        S1 = g1["S"].clone()
+        o1 = torch.empty(1, 4, V, device=dev)
+        dec1 = exts["decode"]
+        scale1 = K ** -0.5
+
+        def step1():  # the same single step from S0 each time (out of place)
+            dec1.forward(g1["q"], g1["k"], g1["v"], g1["a"], g1["b"], g1["A_log"], g1["dt_bias"], g1["S"], scale1,
+                         o1, S1)
+
+        for _ in range(5):
+            step1()
+        ms1 = time_events(step1, 200, torch)
+        gbs1 = decode_bytes(1, 4) / (ms1 / 1e3) / 1e9
+        leg1 = {"config": "config 1: one GDN decode step, B=1 H=4 dk=dv=128, seed 0, S0 ~ N(0, 0.02)",
+                "us_per_step": ms1 * 1e3, "steps_per_s": 1e3 / ms1,
+                "roofline": {"bound": "hbm", "achieved": gbs1, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": gbs1 / PEAK_HBM_GBS, "bytes_per_launch": decode_bytes(1, 4)}}
+        if cpu:
+            from oracle.decode_ref import ref_decode
+
+            def cpu1():
+                return ref_decode(d1["q"].reshape(1, 1, 4, K), d1["k"].reshape(1, 1, 4, K),
+                                  d1["v"].reshape(1, 1, 4, V), d1["S"], d1["A_log"], d1["a"].reshape(1, 1, 4),
+                                  d1["dt_bias"], d1["b"].reshape(1, 1, 4), scale1)
+
+            sec1, (o1_ref, S1_ref) = time_cpu(cpu1, 200)
+            leg1["cpu_baseline"] = dict(value=1 / sec1, unit="steps/s", cores=nthr, kind="port",
+                                        sample=f"oracle.decode_ref.ref_decode on the same inputs, 1 warm-up + 200 "
+                                               f"timed steps, {sec1 * 1e6:.0f} us/step")
+            leg1["parity"] = {"out_max_abs_err": (o1.cpu().reshape(-1) - o1_ref.reshape(-1)).abs().max().item(),
+                              "state_rel_fro": rel_fro(S1.cpu(), S1_ref)}
+        result["decode_cfg1"] = leg1
+        log(f"decode config 1 (B=1 H=4): {ms1 * 1e3:.1f} us/step, parity {leg1.get('parity')}")
+        del d1, g1, S1, o1
+
     # ------------------------------------------------------------------ decode (config 3)
     if "decode" in legs:
         DB, DH = 256, 32
