@@ -195,9 +195,14 @@ __device__ __forceinline__ IntraUnit intra_unit(const PrefillParams& p, int u) {
     return U;
 }
 
+// The wave that computes a unit's gates (one token per lane).  It is the wave
+// with no work in the last round of the triangular solve, where it computes
+// the next unit's gates ahead of time.
+constexpr int kGateWave = 2;
+
 // A unit's global inputs that are prefetched into registers: the K tile slice
-// this thread stores to LDS (rows past the sequence end zero) and wave 0's
-// gate inputs (one token per lane, and A_log of the head).
+// this thread stores to LDS (rows past the sequence end zero) and the gate
+// wave's inputs (one token per lane, and A_log of the head).
 struct IntraLoads {
     u32x4 kv[4];
     float g_m, g_alog;
@@ -207,8 +212,8 @@ __device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUn
     const int wave = tid >> 6, lane = tid & 63;
     L.g_m = L.g_alog = 0.f;
     L.g_a = L.g_b = 0u;
-    if (wave == 0) L.g_alog = p.A_log[U.h];
-    if (wave == 0 && lane < U.nvalid) {
+    if (wave == kGateWave) L.g_alog = p.A_log[U.h];
+    if (wave == kGateWave && lane < U.nvalid) {
         const size_t gi = U.row_base + lane;
         L.g_m = p.mask ? p.mask[static_cast<size_t>(U.sq.b) * p.T_stride + U.sq.tok0 + U.t0 + lane] : 1.f;
         L.g_a = p.a[gi];
@@ -220,6 +225,25 @@ __device__ __forceinline__ void intra_load(const PrefillParams& p, const IntraUn
         L.kv[it] = u32x4{0u, 0u, 0u, 0u};
         if (row < U.nvalid) L.kv[it] = *reinterpret_cast<const u32x4*>(p.k + (U.row_base + row) * kDK + c8);
     }
+}
+
+// A unit's gates, one token per lane (the gate wave): log2 of the in-chunk
+// decay cumsum, beta m, m scale, and the gate block gamma, m scale gamma,
+// gamma_C / gamma.  Tokens past the sequence end: no decay, beta m = m = 0.
+struct GateVals {
+    float lg2, bm, ms, g0, g1, g2;
+};
+__device__ __forceinline__ GateVals gate_vals(const PrefillParams& p, const IntraLoads& L, int lane, int nvalid) {
+    float lg = 0.f, bm = 0.f, m = 0.f;
+    if (lane < nvalid) {
+        m = L.g_m;
+        lg = -expf(L.g_alog) * softplus_f(__uint_as_float(L.g_a << 16) + p.dt_bias);
+        bm = sigmoid_f(__uint_as_float(L.g_b << 16)) * m;
+    }
+    const float s = wave_inclusive_sum(lg);
+    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), kWave - 1));
+    const float gam = expf(s);
+    return {s * 1.4426950408889634f, bm, m * p.scale, gam, m * p.scale * gam, expf(last - s)};
 }
 
 // Tp fragments (mt, s) = (wave, 0), (wave, 1) of one record: fragments
@@ -279,6 +303,8 @@ gdn_prefill_intra_kernel(PrefillParams p) {
     u32x4 tpf[2];          // the previous unit's Tp fragments 2 wave, 2 wave + 1
     size_t wc_prev = 0;
     bool have_prev = false;
+    GateVals gv = {};      // gate wave: this unit's gates, computed ahead during the previous unit
+    bool gv_ready = false;
     while (u < p.intra_units) {
     const int u_next = u + static_cast<int>(gridDim.x);
     const IntraUnit N = intra_unit(p, u_next);
@@ -290,10 +316,8 @@ gdn_prefill_intra_kernel(PrefillParams p) {
     }
     const int c = U.c, h = U.h, nvalid = U.nvalid;
     const size_t wc = U.wc;
-    const bool tok_ok = wave == 0 && lane < nvalid;
-    const float g_m = L.g_m, g_alog = L.g_alog;
-    const float g_a = __uint_as_float(L.g_a << 16), g_b = __uint_as_float(L.g_b << 16);
     (void)c;
+    (void)h;
 
     // 1) K tile into LDS.
 #pragma unroll
@@ -317,27 +341,14 @@ gdn_prefill_intra_kernel(PrefillParams p) {
         for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * s));
     }
 
-    // 2) Gates (wave 0, one token per lane) and the in-chunk log-cumsum.
-    float G0 = 0.f, G1 = 0.f, G2 = 0.f, H0 = 0.f, H1 = 0.f;  // this unit's gate and token rows, stored after step 3
-    if (wave == 0) {
-        const int t = lane;
-        float lg = 0.f, bm = 0.f, m = 0.f;
-        if (tok_ok) {
-            m = g_m;
-            lg = -expf(g_alog) * softplus_f(g_a + p.dt_bias);
-            bm = sigmoid_f(g_b) * m;
-        }
-        const float s = wave_inclusive_sum(lg);
-        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), kWave - 1));
-        s_lg2[t] = s * 1.4426950408889634f;  // log2(e)
-        s_bm[t] = bm;
-        s_ms[t] = m * p.scale;
-        H0 = s * 1.4426950408889634f;
-        H1 = m * p.scale;
-        const float gam = expf(s);
-        G0 = gam;
-        G1 = m * p.scale * gam;
-        G2 = expf(last - s);
+    // 2) Gates and the in-chunk log-cumsum (the gate wave, one token per
+    //    lane; computed during the previous unit's last solve round when that
+    //    unit ran here).
+    if (wave == kGateWave) {
+        if (!gv_ready) gv = gate_vals(p, L, lane, nvalid);
+        s_lg2[lane] = gv.lg2;
+        s_bm[lane] = gv.bm;
+        s_ms[lane] = gv.ms;
     }
     __syncthreads();
 
@@ -382,15 +393,15 @@ gdn_prefill_intra_kernel(PrefillParams p) {
     // The current unit's inputs are consumed: start the next unit's loads,
     // then this unit's stores.
     if (N.valid) intra_load(p, N, tid, L);
-    if (wave == 0) {
+    if (wave == kGateWave) {
         float* G = reinterpret_cast<float*>(p.wsR + (wc * RF + RG) * 64);
-        G[lane] = G0;
-        G[64 + lane] = G1;
-        G[128 + lane] = G2;
+        G[lane] = gv.g0;
+        G[64 + lane] = gv.g1;
+        G[128 + lane] = gv.g2;
         if constexpr (!AQ) {
             float* Hb = reinterpret_cast<float*>(p.wsR + (wc * RF + kRecH) * 64);
-            Hb[lane] = H0;
-            Hb[64 + lane] = H1;
+            Hb[lane] = gv.lg2;
+            Hb[64 + lane] = gv.ms;
         }
     }
     if (have_prev) store_tp<RF>(p, wc_prev, wave, lane, tpf);
@@ -532,8 +543,12 @@ gdn_prefill_intra_kernel(PrefillParams p) {
             put_tp(3, 0, mul_tw(mul_tw(zero, 5, w2), 3, w3));
         } else if (wave == 3) {
             put_tp(3, 1, mul_tw(x, 5, w2));
+        } else if (N.valid) {  // the gate wave (no product here): the next unit's gates
+            static_assert(kGateWave == 2, "the gate wave is the one idle in this round");
+            gv = gate_vals(p, L, lane, N.nvalid);
         }
     }
+    gv_ready = N.valid;
     __syncthreads();
 
     // 6) Tp fragments, two per wave, stored with the next unit's stores.
