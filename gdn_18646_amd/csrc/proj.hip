@@ -202,6 +202,8 @@ constexpr int kMStageB = (kMCols + kMToks) * kMRowB;  // 64 KiB: W rows, then x 
 constexpr int kMDma = (kMCols + kMToks) / 8 / kMWaves;  // 1 KiB copies (8 rows) per wave per stage
 static_assert((kMCols + kMToks) % (8 * kMWaves) == 0 && kMCols % (8 * kMWaves) == 0, "copies split evenly");
 static_assert(kMToks == 2 * 16 * kWNT, "two token waves");
+constexpr int kMHandB = (kMCols / (16 * kWMT)) * kWMT * 1024;  // hand-over area: one 16-token fp32 tile per column wave and MFMA tile
+static_assert(kMStages * kMStageB == kMToks * kMCols * 2, "the stages hold the bf16 output tile");
 
 // Staged row r holds its 8 16-byte chunks (k 8c .. 8c+7) at slot c ^ (r & 7):
 // a fragment read (16 rows, one chunk each) then spreads every 8 consecutive
@@ -218,6 +220,13 @@ __device__ __forceinline__ float tap_prev(float cur, float prev) {
     return __int_as_float(__builtin_amdgcn_update_dpp(rot, __float_as_int(cur), 0x110 + K, 0xf, 0xf, false));
 }
 
+// Groups whose output goes out through the LDS output tile in 16-byte
+// chunks: 8-column aligned, 8-column head_dim (or token-major), 16-byte
+// aligned destination.
+__device__ __forceinline__ bool staged_group(const gdn_proj::ProjGroup& g) {
+    return ((g.col0 | g.width | g.head_dim) & 7) == 0 && (reinterpret_cast<uintptr_t>(g.dst) & 15) == 0;
+}
+
 // The group holding column c, by compare-and-select over constant indices
 // (indexing the parameter block with a runtime index would copy it to
 // private memory).
@@ -231,7 +240,7 @@ __device__ __forceinline__ gdn_proj::ProjGroup select_group(const gdn_proj::Proj
 
 __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kMWaves / 4, kMWaves / 4))) void gdn_proj_conv_mfma_kernel(
     gdn_proj::ProjParams p, int n_tok, int n_col) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[kMStages * kMStageB];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[kMStages * kMStageB + kMHandB];
     lds_u8* const smem = (lds_u8*)&smem_raw[0];
 
     // Workgroup -> tile.  Dispatch deals workgroups to the 8 XCDs round-robin;
@@ -368,15 +377,15 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
     }
 
     // The token waves meet at token 128: the wn = 1 wave's first tile takes
-    // its conv taps from the wn = 0 wave's last tile, handed over through the
-    // stage the last K step did not read (no copy targets it any more).
-    const lds_u8* xs = smem + (nk & 1) * kMStageB + wm * kWMT * 1024 + lane * 16;
+    // its conv taps from the wn = 0 wave's last tile, handed over through an
+    // LDS area of its own (the stages become the output tile below).
+    const lds_u8* xs = smem + kMStages * kMStageB + wm * kWMT * 1024 + lane * 16;
     if (wn == 0) {
 #pragma unroll
         for (int mt = 0; mt < kWMT; ++mt)
             *reinterpret_cast<lds_f32x4*>(const_cast<lds_u8*>(xs) + mt * 1024) = acc[mt][kWNT - 1];
     }
-    lds_barrier();
+    lds_barrier();  // hand-over written; every wave is past its last stage read
 
     // This lane's row in token tile 0 of the wave, as (b, t3 = t + 3); tile
     // nt adds 16 rows.  Rows before local row kHalo are the tile's halo.
@@ -401,6 +410,13 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         lean = R0 >= 0 && R0 + 16 * kWNT <= F3 && t3R >= kHalo && t3R + 16 * kWNT <= T3 - ncache;
     }
 
+    // Output tile in LDS (the two stages): row = token of the tile (512
+    // bytes, 256 columns bf16), 32-byte unit u of a row stored at unit
+    // u ^ (row & 15), so the 16 tokens of a fragment write spread over the
+    // banks and a row reads back whole.
+    lds_u8* const otile = smem;
+    auto ounit = [](int row, int u) { return row * 512 + ((u ^ (row & 15)) << 5); };
+
     static_for<0, kWMT>([&](auto MT) {
         constexpr int mt = decltype(MT)::value;
         const int cb = c0 + 16 * kWMT * wm + 16 * mt + 4 * g4;  // this lane's 4 columns (same for the whole DPP row)
@@ -408,24 +424,7 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         const gdn_proj::ProjGroup gq = select_group(p, cb);
         const int cc = cb - gq.col0, width = gq.width, hd = gq.head_dim;
         const bool conv = gq.conv != 0;
-        // Element index of (b, t, column cc + i): b width T + t tstride + coff[i]
-        // (token-major: tstride = width, coff = cc + i; head-major [B, width/hd,
-        // T, hd]: tstride = hd, coff = ((cc + i) / hd) T hd + (cc + i) % hd).
-        const size_t seq = static_cast<size_t>(width) * p.T_out;
-        const int tstride = hd ? hd : width;
-        const bool vec = hd == 0 || (hd & 3) == 0;  // the 4 columns are adjacent in memory
-        size_t coff[4];
-        {
-            int h = hd ? cc / hd : 0, d = hd ? cc - h * hd : cc;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                coff[i] = hd ? static_cast<size_t>(h) * p.T_out * hd + d : static_cast<size_t>(cc + i);
-                if (hd && ++d == hd) {
-                    d = 0;
-                    ++h;
-                }
-            }
-        }
+        const bool staged = staged_group(gq);
         float w[4][4];  // [column][tap], taps right-aligned: tap 3 multiplies the current token
         if (p.conv_k == 4) {
 #pragma unroll
@@ -464,8 +463,50 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         };
         f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
         if (wn == 1) pv = cache_row(*reinterpret_cast<const lds_f32x4*>(xs + mt * 1024), bx, t3x);
-        // conv + SiLU of one 16-token tile (plain groups: the current row).
-        auto finish = [&](const f32x4 cur, float (&y)[4]) {
+        // Unstaged groups (head_dim 1..3 or 4-column aligned only) store from
+        // registers.  Element index of (b, t, column cc + i): b width T + t
+        // tstride + coff[i] (token-major: tstride = width, coff = cc + i;
+        // head-major [B, width/hd, T, hd]: tstride = hd, coff = ((cc + i) /
+        // hd) T hd + (cc + i) % hd).
+        const size_t seq = static_cast<size_t>(width) * p.T_out;
+        const int tstride = hd ? hd : width;
+        const bool vec = hd == 0 || (hd & 3) == 0;  // the 4 columns are adjacent in memory
+        size_t coff[4] = {0, 0, 0, 0};
+        if (!staged) {
+            int h = hd ? cc / hd : 0, d = hd ? cc - h * hd : cc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                coff[i] = hd ? static_cast<size_t>(h) * p.T_out * hd + d : static_cast<size_t>(cc + i);
+                if (hd && ++d == hd) {
+                    d = 0;
+                    ++h;
+                }
+            }
+        }
+        auto store = [&](uint16_t* row, const float (&y)[4]) {
+            if (vec) {
+                *reinterpret_cast<u32x2*>(row + coff[0]) = u32x2{pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3])};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) row[coff[i]] = f2bf_bits(y[i]);
+            }
+        };
+        const int unit = 4 * wm + mt;  // 32-byte unit of the output row holding this fragment's columns
+        int b = b0, t3 = t30;
+        static_for<0, kWNT>([&](auto NT) {
+            constexpr int nt = decltype(NT)::value;
+            if (nt > 0 && !lean) {
+                t3 += 16;
+                if (t3 >= T3) {
+                    b += t3 / T3;
+                    t3 %= T3;
+                }
+            }
+            const int nloc = nloc0 + 16 * nt;
+            f32x4 cur = acc[mt][nt];
+            if (!lean) cur = cache_row(cur, b, t3);
+            // conv + SiLU (plain groups: the current row)
+            float y[4];
             if (conv) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -477,52 +518,20 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
 #pragma unroll
                 for (int i = 0; i < 4; ++i) y[i] = cur[i];
             }
-        };
-        auto store = [&](uint16_t* row, const float (&y)[4]) {
-            if (vec) {
-                *reinterpret_cast<u32x2*>(row + coff[0]) = u32x2{pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3])};
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) row[coff[i]] = f2bf_bits(y[i]);
-            }
-        };
-        if (lean) {
-            // The wave's rows are tokens of one sequence, clear of its cache
-            // rows and of the cache refresh window: no per-row checks.
-            uint16_t* const row0 = gq.dst + static_cast<size_t>(b0) * seq + static_cast<size_t>(t30 - kHalo) * tstride;
-            static_for<0, kWNT>([&](auto NT) {
-                constexpr int nt = decltype(NT)::value;
-                const f32x4 cur = acc[mt][nt];
-                float y[4];
-                finish(cur, y);
-                pv = cur;
-                if (nt == 0 && nloc0 < kHalo) return;  // the tile's halo rows
-                store(row0 + static_cast<size_t>(16 * nt) * tstride, y);
-            });
-            return;
-        }
-        int b = b0, t3 = t30;
-        static_for<0, kWNT>([&](auto NT) {
-            constexpr int nt = decltype(NT)::value;
-            if (nt > 0) {
-                t3 += 16;
-                if (t3 >= T3) {
-                    b += t3 / T3;
-                    t3 %= T3;
-                }
-            }
-            const int nloc = nloc0 + 16 * nt;
-            const bool row_ok = nloc >= kHalo && f0 + nloc < F3;  // a row this tile owns
-            const int t = t3 - kHalo;
-            const f32x4 cur = cache_row(acc[mt][nt], b, t3);
-            float y[4];
-            finish(cur, y);
             pv = cur;
-            if (!row_ok) return;
-            if (t >= 0) store(gq.dst + static_cast<size_t>(b) * seq + static_cast<size_t>(t) * tstride, y);
+            if (staged) {
+                *reinterpret_cast<lds_u32x2*>(otile + ounit(nloc, unit) + 8 * g4) =
+                    u32x2{pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3])};
+            } else if (lean) {
+                if (!(nt == 0 && nloc0 < kHalo))  // the tile's halo rows
+                    store(gq.dst + static_cast<size_t>(b0) * seq + static_cast<size_t>(t30 - kHalo + 16 * nt) * tstride, y);
+            } else if (nloc >= kHalo && f0 + nloc < F3 && t3 >= kHalo) {
+                store(gq.dst + static_cast<size_t>(b) * seq + static_cast<size_t>(t3 - kHalo) * tstride, y);
+            }
             // New cache: rows t = T - ncache .. T - 1 of the extended sequence
             // (cache rows included when T < ncache).
-            if (conv && gq.cache_out && t >= p.T - ncache) {
+            if (!lean && conv && gq.cache_out && nloc >= kHalo && f0 + nloc < F3 && t3 - kHalo >= p.T - ncache) {
+                const int t = t3 - kHalo;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     gq.cache_out[(static_cast<size_t>(b) * width + cc + i) * ncache + (t - (p.T - ncache))] =
@@ -530,6 +539,41 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             }
         });
     });
+    lds_barrier();  // output tile complete
+
+    // Store the tile's staged columns row by row: thread tid takes 16-byte
+    // chunk j = tid % 32 (8 columns) of tile rows tid / 32 + 16 i, so a wave
+    // writes two whole 512-byte rows per instruction (for head-major groups,
+    // two 256-byte token rows of each head).
+    {
+        const int j = tid & 31;
+        const int c = c0 + 8 * j;
+        if (c >= p.D_out) return;
+        const gdn_proj::ProjGroup gq = select_group(p, c);
+        if (!staged_group(gq)) return;
+        const int cc = c - gq.col0, hd = gq.head_dim;
+        const size_t seq = static_cast<size_t>(gq.width) * p.T_out;
+        const size_t tstride = hd ? hd : gq.width;
+        uint16_t* const colp = gq.dst + (hd ? static_cast<size_t>(cc / hd) * p.T_out * hd + cc % hd : static_cast<size_t>(cc));
+        const int row0 = tid >> 5;
+        int b, t3;
+        split(f0 + row0, b, t3);
+#pragma unroll 4
+        for (int i = 0; i < kMToks / 16; ++i) {
+            const int row = row0 + 16 * i;
+            if (i > 0) {
+                t3 += 16;
+                while (t3 >= T3) {
+                    t3 -= T3;
+                    ++b;
+                }
+            }
+            if (row >= kHalo && f0 + row < F3 && t3 >= kHalo) {
+                const u32x4 v = *reinterpret_cast<const lds_u32x4*>(otile + ounit(row, j >> 1) + 16 * (j & 1));
+                *reinterpret_cast<u32x4*>(colp + static_cast<size_t>(b) * seq + static_cast<size_t>(t3 - kHalo) * tstride) = v;
+            }
+        }
+    }
 }
 
 }  // namespace
