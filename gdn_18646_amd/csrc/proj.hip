@@ -19,7 +19,8 @@
 // Waves form a 4 x 2 grid of 64 columns x 128 tokens = 4 x 8 MFMA 16x16x32
 // tiles.  In the transposed C layout a lane holds 4 adjacent columns of one
 // token and the 16 tokens of a tile form one DPP row: the conv taps are row
-// shifts, and stores are 8 bytes.
+// shifts.  The bf16 results go into an output tile in LDS (the two stages)
+// and leave as whole rows, 16 bytes per lane.
 //
 // gdn_proj_conv_kernel (general shapes: group boundaries not on 4 columns,
 // unaligned outputs, K not a multiple of 64) computes 128 x 128 tiles of P whose rows are
