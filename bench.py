@@ -24,9 +24,12 @@ same-run parity of the GPU results against that oracle:
 * ``layer_e2e``: config 5, the whole layer (RMSNorm, fused projection + conv
   + SiLU, prefill, output projection) at B=4 x T=4096, then decode steps at
   B=4 continuing from the prefill state.
+* ``layer_decode_batches``: the layer's decode step at config-5 dims for
+  B = 1, 8, 32, 64, 128, 256 (the reference's serving sweep), HBM roofline
+  per B, parity against the oracle layer at B=256.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--no-extra] [--only prefill,cfg2,batches,varlen,decode,layer]
+                    [--no-extra] [--only prefill,cfg2,batches,varlen,decode,layer,serve]
 """
 
 import argparse
@@ -56,7 +59,7 @@ def decode_bytes(B, H):
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-LEGS = ("prefill", "cfg2", "batches", "varlen", "decode", "layer")
+LEGS = ("prefill", "cfg2", "batches", "varlen", "decode", "layer", "serve")
 
 
 def measured_traffic(kernel):
@@ -124,6 +127,80 @@ def roofline_fracs(flop, nbytes, ms):
     tf = flop / (ms / 1e3) / 1e12
     gbs = nbytes / (ms / 1e3) / 1e9
     return {"tflops": tf, "mfma_frac": tf / PEAK_BF16_TFLOPS, "gbs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS}
+
+
+def serve_leg(exts, dev, cpu, nthr, torch):
+    """GDNLayerCustom.decode at B in {1, 8, 32, 64, 128, 256}, config-5 dims (the
+    reference's layer decode sweep, bench_gdn.py:332-342): one step = RMSNorm,
+    q/k/v/a/b projection + conv step, the recurrence (state in place), W_o.
+    B <= 16 runs the fused step (two skinny projection kernels around the
+    recurrence), larger B the library GEMMs around the conv-step and
+    recurrence kernels.  Roofline: HBM, algorithmic bytes per step = both
+    weight matrices + the fp32 state read and written + x in and y out.
+    Parity at B=256: two steps from the same state against the oracle layer's
+    decode (fp32 projection), which is also the CPU baseline."""
+    from gdn_18646_amd.gdn_layer import GDNLayerCustom, make_weights
+    LD, LH = 2048, 16
+    gs = torch.Generator().manual_seed(6)
+    w_cpu = make_weights(device="cpu", D=LD, H=LH, DK=128, DV=128, std=0.02, generator=gs)
+    layer = GDNLayerCustom({k: v.to(dev) for k, v in w_cpu.items()}, exts)
+    ncols = 2 * LH * 128 + LH * 128 + 2 * LH
+    wbytes = 2 * ncols * LD + 2 * LD * LH * 128
+
+    def state_for(SB):
+        st = {k: v.cpu() for k, v in layer.init_decode_state(SB).items()}
+        st["recurrent"].normal_(0.0, 0.02, generator=gs)
+        for key in ("conv_q", "conv_k", "conv_v", "xn"):
+            st[key].copy_(torch.randn(st[key].shape, generator=gs) * 0.5)
+        return st
+
+    leg = {"config": "GDNLayerCustom.decode, hidden 2048, H=16, dk=dv=128, conv 4, weights N(0, 0.02), fp32 state "
+                     "N(0, 0.02) updated in place, fresh x N(0, 1) each step",
+           "bytes_per_step": "2 (W_qkvab + W_o) + B H 128 128 4 x 2 (state read + write) + 4 B D (x, y)"}
+    for SB in (1, 8, 32, 64, 128, 256):
+        st = {k: v.to(dev) for k, v in state_for(SB).items()}
+        xs = [torch.randn(SB, 1, LD, generator=gs).bfloat16().to(dev) for _ in range(8)]
+        it = iter(range(10 ** 9))
+
+        def step():
+            layer.decode(xs[next(it) % len(xs)], st, inplace=True)
+
+        for _ in range(3):
+            step()
+        ms = time_events(step, 100 if SB <= 64 else 50, torch)
+        nbytes = wbytes + SB * LH * 128 * 128 * 4 * 2 + 4 * SB * LD
+        leg[f"B{SB}"] = {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "tokens_per_s": SB * 1e3 / ms,
+                         "gbs": nbytes / (ms * 1e6), "hbm_frac": nbytes / (ms * 1e6) / PEAK_HBM_GBS,
+                         "bytes": nbytes, "path": "fused step" if SB <= 16 and layer.fused_decode else "unfused"}
+        log(f"layer decode B={SB}: {ms * 1e3:.1f} us/step, {nbytes / (ms * 1e6):.0f} GB/s")
+        del st, xs
+    # parity and CPU baseline at B=256
+    SB = 256
+    st_cpu = state_for(SB)
+    x2 = [torch.randn(SB, 1, LD, generator=gs).bfloat16() for _ in range(2)]
+    st = {k: v.to(dev) for k, v in st_cpu.items()}
+    ys = []
+    for x in x2:
+        y, st = layer.decode(x.to(dev), st)
+        ys.append(y.cpu())
+    torch.cuda.synchronize()
+    from oracle.layer_ref import GDNLayerBaseline
+    base = GDNLayerBaseline(w_cpu, fp32_proj=True)
+    st_ref, ys_ref, secs = st_cpu, [], []
+    for x in x2:
+        t0 = time.perf_counter()
+        y_ref, st_ref = base.decode(x, st_ref)
+        secs.append(time.perf_counter() - t0)
+        ys_ref.append(y_ref)
+    y_g, y_r = torch.cat(ys, 1), torch.cat(ys_ref, 1)
+    leg["parity_B256_2steps"] = {**out_parity(y_g, y_r), "rel_fro": rel_fro(y_g, y_r),
+                                 "state_rel_fro": rel_fro(st["recurrent"], st_ref["recurrent"])}
+    if cpu:
+        leg["cpu_baseline"] = dict(value=1.0 / secs[-1], unit="steps/s", cores=nthr, kind="port",
+                                   sample=f"oracle.layer_ref.GDNLayerBaseline.decode (fp32 projection) at B=256 on "
+                                          f"the same state and inputs, second of two steps, {secs[-1] * 1e3:.0f} ms")
+    log(f"  layer decode parity {leg['parity_B256_2steps']}")
+    return leg
 
 
 def main():
@@ -462,15 +539,6 @@ def main():
         for _ in range(3):
             layer_dec()
         ms_ld = time_events(layer_dec, 128, torch)
-        step_g = layer.capture_decode(st_l)
-        it_g = iter(range(10 ** 9))
-
-        def layer_dec_graph():
-            step_g(xd[next(it_g) % len(xd)])
-
-        for _ in range(3):
-            layer_dec_graph()
-        ms_ldg = time_events(layer_dec_graph, 128, torch)
         ncols = 2 * LH * 128 + LH * 128 + 2 * LH
         lflop = (2 * LB * LT * LD * ncols + PREFILL_FLOP_PER_TOKEN_HEAD * LB * LT * LH + 2 * LB * LT * LH * 128 * LD)
         lbytes = (2 * LB * LT * LD * 2 + 2 * ncols * LD + 2 * LD * LH * 128 +
@@ -481,11 +549,9 @@ def main():
                "prefill_ms": ms_lf, "prefill_tokens_per_s": LB * LT / (ms_lf / 1e3),
                "prefill_roofline": {**roofline_fracs(lflop, lbytes, ms_lf), "flop": lflop, "bytes": lbytes},
                "decode_ms_per_step": ms_ld, "decode_steps_per_s": 1e3 / ms_ld,
-               "decode_roofline": {**roofline_fracs(0, dbytes, ms_ld), "bytes": dbytes},
-               "decode_graph_ms_per_step": ms_ldg, "decode_graph_steps_per_s": 1e3 / ms_ldg}
+               "decode_roofline": {**roofline_fracs(0, dbytes, ms_ld), "bytes": dbytes}}
         log(f"layer (config 5): prefill B={LB} T={LT} {ms_lf:.3f} ms ({LB * LT / (ms_lf / 1e3):.4g} tok/s), "
-            f"decode B={LB} {ms_ld * 1e3:.1f} us/step eager, {ms_ldg * 1e3:.1f} us/step as a HIP graph")
-        del step_g
+            f"decode B={LB} {ms_ld * 1e3:.1f} us/step")
         # decode == prefill at config 5: 32 decode steps from the prefill state of the
         # first 4064 tokens against the forward over all 4096 (GPU against GPU)
         _, st_full = layer.forward(xl, return_state=True)  # st_l was advanced by the timed decode steps
@@ -511,6 +577,10 @@ def main():
         result["layer_e2e"] = leg
         log(f"  layer parity {leg['parity']}")
         del layer, wl, xl, st_l
+
+    # ------------------------------- layer decode at serving batch sizes (config-5 dims)
+    if "serve" in legs:
+        result["layer_decode_batches"] = serve_leg(exts, dev, cpu, nthr, torch)
 
     line = {
         "metric": "prefill tokens/s (T=8192) + decode steps/s (B=256); % of MFMA / HBM roofline",

@@ -134,12 +134,11 @@ __global__ __launch_bounds__(kWave* kWavesPerWG) void gdn_decode_kernel(
 
 }  // namespace
 
-extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
-                              const gdn_bf16_t* a, const gdn_bf16_t* b, const float* A_log,
-                              const float* dt_bias, const float* S_in, float scale, float* o,
-                              float* S_out, int B, int H, int dk, int dv, void* stream) {
-    using gdn_host::aligned;
-    using gdn_host::fail;
+namespace gdn_host {
+
+int decode_check(const void* q, const void* k, const void* v, const void* a, const void* b, const void* A_log,
+                 const void* dt_bias, const void* S_in, const void* o, const void* S_out, int B, int H, int dk,
+                 int dv) {
     if (B < 0 || H <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "decode: B=%d H=%d", B, H);
     if (dk != kDK) return fail(GDN_ERR_UNSUPPORTED, "decode: dk=%d, only dk=128 is built", dk);
     if (dv < 32 || dv > 1024 || dv % 32 != 0)
@@ -150,6 +149,18 @@ extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gd
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 8) || !aligned(S_in, 16) ||
         !aligned(S_out, 16) || !aligned(o, 16))
         return fail(GDN_ERR_INVALID_ARGUMENT, "decode: q/k/S/o need 16-byte, v 8-byte alignment");
+    return GDN_OK;
+}
+
+}  // namespace gdn_host
+
+extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                              const gdn_bf16_t* a, const gdn_bf16_t* b, const float* A_log,
+                              const float* dt_bias, const float* S_in, float scale, float* o,
+                              float* S_out, int B, int H, int dk, int dv, void* stream) {
+    using gdn_host::fail;
+    const int chk = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
+    if (chk != GDN_OK || B == 0) return chk;
     // Column slice: the widest of 128 / 64 / 32 dividing dv, halved while the
     // grid would leave CUs idle (a small batch splits each head's columns
     // over more workgroups; columns of the state update independently).

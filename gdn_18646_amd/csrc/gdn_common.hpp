@@ -190,4 +190,9 @@ namespace gdn_host {
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char* kernel);
 inline bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+// Argument checks of gdn_decode_hip (defined in decode.hip): GDN_OK when the
+// call would launch (or, for B == 0, do nothing), else the error status.
+int decode_check(const void* q, const void* k, const void* v, const void* a, const void* b, const void* A_log,
+                 const void* dt_bias, const void* S_in, const void* o, const void* S_out, int B, int H, int dk,
+                 int dv);
 }  // namespace gdn_host

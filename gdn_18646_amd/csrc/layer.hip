@@ -519,11 +519,13 @@ extern "C" int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* c
     return gdn_host::check_launch("gdn_decode_conv_step_kernel");
 }
 
-extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps,
-                                      const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q,
-                                      gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, gdn_bf16_t* xn_hist, gdn_bf16_t* q,
-                                      gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, int B, int D, int H,
-                                      int dk, int dv, int conv_k, void* stream) {
+namespace {
+
+// Argument checks of the decode-step projections: GDN_OK when the call would
+// launch (or, for B == 0, do nothing), else the error status.
+int in_proj_check(const void* x, const void* gamma, const void* W_qkvab, const void* conv_w_qkv, const void* cache_q,
+                  const void* cache_k, const void* cache_v, const void* q, const void* k, const void* v, const void* a,
+                  const void* b, int B, int D, int H, int dk, int dv, int conv_k) {
     using gdn_host::aligned;
     using gdn_host::fail;
     if (B < 0 || D <= 0 || H <= 0 || dk <= 0 || dv <= 0)
@@ -541,6 +543,34 @@ extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gam
         return fail(GDN_ERR_INVALID_ARGUMENT, "decode_in_proj: null pointer argument");
     if (!aligned(x, 16) || !aligned(gamma, 16) || !aligned(W_qkvab, 16))
         return fail(GDN_ERR_INVALID_ARGUMENT, "decode_in_proj: x/gamma/W need 16-byte alignment");
+    return GDN_OK;
+}
+
+int out_proj_check(const void* o, const void* W_o, const void* y, int B, int K, int N) {
+    using gdn_host::aligned;
+    using gdn_host::fail;
+    if (B < 0 || K <= 0 || N <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: B=%d K=%d N=%d", B, K, N);
+    if (B > kSkM) return fail(GDN_ERR_UNSUPPORTED, "decode_out_proj: B=%d, at most %d sequences", B, kSkM);
+    if (K % 32 != 0 || K > kSkStride * 16)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_out_proj: K=%d must be a multiple of 32, at most %d", K,
+                    kSkStride * 16);
+    if (B == 0) return GDN_OK;
+    if (!o || !W_o || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: null pointer argument");
+    if (!aligned(o, 16) || !aligned(W_o, 16))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: o/W need 16-byte alignment");
+    return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps,
+                                      const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q,
+                                      gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, gdn_bf16_t* xn_hist, gdn_bf16_t* q,
+                                      gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, int B, int D, int H,
+                                      int dk, int dv, int conv_k, void* stream) {
+    const int chk = in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B, D, H,
+                                  dk, dv, conv_k);
+    if (chk != GDN_OK || B == 0) return chk;
     SkinnyParams p = {};
     p.W = W_qkvab;
     p.B = B;
@@ -569,17 +599,8 @@ extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gam
 
 extern "C" int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W_o, gdn_bf16_t* y, int B, int K, int N,
                                        void* stream) {
-    using gdn_host::aligned;
-    using gdn_host::fail;
-    if (B < 0 || K <= 0 || N <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: B=%d K=%d N=%d", B, K, N);
-    if (B > kSkM) return fail(GDN_ERR_UNSUPPORTED, "decode_out_proj: B=%d, at most %d sequences", B, kSkM);
-    if (K % 32 != 0 || K > kSkStride * 16)
-        return fail(GDN_ERR_UNSUPPORTED, "decode_out_proj: K=%d must be a multiple of 32, at most %d", K,
-                    kSkStride * 16);
-    if (B == 0) return GDN_OK;
-    if (!o || !W_o || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: null pointer argument");
-    if (!aligned(o, 16) || !aligned(W_o, 16))
-        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_out_proj: o/W need 16-byte alignment");
+    const int chk = out_proj_check(o, W_o, y, B, K, N);
+    if (chk != GDN_OK || B == 0) return chk;
     SkinnyParams p = {};
     p.W = W_o;
     p.B = B;
@@ -597,9 +618,15 @@ extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* 
                                          float scale, const gdn_bf16_t* W_o, gdn_bf16_t* q, gdn_bf16_t* k,
                                          gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, float* o, gdn_bf16_t* y, int B,
                                          int D, int H, int dk, int dv, int conv_k, void* stream) {
-    // The three launches validate their own arguments; the first failure
-    // returns before anything later is launched.
-    int st = gdn_decode_in_proj_hip(x, gamma, eps, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v,
+    // Every stage's arguments are checked before the first launch: the
+    // in-projection updates the conv caches and x_n history in place, so a
+    // later stage refusing its arguments would leave the state half-advanced.
+    int st = in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B, D, H, dk, dv,
+                           conv_k);
+    if (st == GDN_OK) st = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
+    if (st == GDN_OK) st = out_proj_check(o, W_o, y, B, H * dv, D);
+    if (st != GDN_OK || B == 0) return st;
+    st = gdn_decode_in_proj_hip(x, gamma, eps, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v,
                                     a, b, B, D, H, dk, dv, conv_k, stream);
     if (st != GDN_OK) return st;
     st = gdn_decode_hip(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, S_out, B, H, dk, dv, stream);

@@ -749,11 +749,8 @@ __device__ __forceinline__ bf16x8 pack8_lo(const f32x4 lo, const f32x4 hi, const
 // the MFMA chain that does depend on it rarely waits on LDS, without holding
 // every fragment in registers at once.  `v_zero`: the tile has no V (identity
 // columns of the map pass).  `next` issues the following chunk's copies.
-// LATE_Q: P = Q S is formed after dV instead of with K S, so that the two
-// waves sharing a SIMD (waves w and w + 4) read the staged fragments at
-// different times instead of all waves loading K and Q at once.
-template <int MODE, int NW, int NT, bool LATE_Q>
-__device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int orow, int nvalid,
+template <int MODE, int NW, int NT>
+__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int orow, int nvalid,
                                             int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
                                             const Stager<MODE, NW, NT>& next) {
     using St = Stage<MODE, NW, NT>;
@@ -763,7 +760,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
 
     next.issue();
 
-    // (a) X = K S (and P = Q S for the output unless LATE_Q), in two k-halves so only half
+    // (a) X = K S (and P = Q S for the output), in two k-halves so only half
     //     of the K and Q fragments is held at a time.
     f32x4 X[4][NT], P[4][NT];
 #pragma unroll
@@ -779,7 +776,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
             for (int s2 = 0; s2 < 2; ++s2) {
                 const int f = 4 * mt + 2 * half + s2;
                 kf[mt][s2] = kfrag(buf + St::offK, f, lane);
-                if constexpr (St::out && !LATE_Q) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
+                if constexpr (St::out) qf[mt][s2] = frag(buf, St::offQ + f * kFragB, lane);
             }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
@@ -792,7 +789,7 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     X[mt][nt] = mfma16x16x32(kf[mt][s2], Bs[nt], X[mt][nt]);
-                    if constexpr (St::out && !LATE_Q) P[mt][nt] = mfma16x16x32(Bs[nt], qf[mt][s2], P[mt][nt]);
+                    if constexpr (St::out) P[mt][nt] = mfma16x16x32(Bs[nt], qf[mt][s2], P[mt][nt]);
                 }
         }
     }
@@ -867,20 +864,6 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
         BS0[nt] = pack8(kd[0] * D[0][nt], kd[1] * D[1][nt]);
         BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
     }
-    if constexpr (St::out && LATE_Q) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            bf16x8 Bs[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const bf16x8 q = frag(buf, St::offQ + (4 * mt + s) * kFragB, lane);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) P[mt][nt] = mfma16x16x32(Bs[nt], q, P[mt][nt]);
-            }
-        }
-    }
     if constexpr (!kEarlyKt) load_kt();
     // (e) S <- gamma_C S + K^T (decay o dV)  (issued before (d): the recurrence's critical path).
 #pragma unroll
@@ -922,16 +905,6 @@ __device__ __forceinline__ void state_chunk_impl(const lds_u8* buf, f32x4 (&S)[8
             }
         }
     }
-}
-
-template <int MODE, int NW, int NT>
-__device__ __forceinline__ void state_chunk(const lds_u8* buf, f32x4 (&S)[8][NT], uint16_t* ob, int orow, int nvalid,
-                                            int wave, int lane, int col0_wave, bool v_zero, uint32_t kt_lane,
-                                            const Stager<MODE, NW, NT>& next) {
-    if (MODE == kModeOut && NW == 8 && wave >= 4)
-        state_chunk_impl<MODE, NW, NT, true>(buf, S, ob, orow, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
-    else
-        state_chunk_impl<MODE, NW, NT, false>(buf, S, ob, orow, nvalid, wave, lane, col0_wave, v_zero, kt_lane, next);
 }
 
 // Work decomposition of the state pass.
@@ -1957,15 +1930,13 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact,
         s.G = G < 2 ? 1 : static_cast<int>(G);
         return s;
     }
-    // Two waves per SIMD (8-wave workgroups) where the tiling allows: the
-    // waves hide each other's LDS and copy latency.  The output pass then
-    // uses 16-column waves, the map pass 32-column waves, both within 256
-    // registers a wave.  Otherwise one wave per SIMD with wider tiles.
-    if (dv % 128 == 0) {
-        s.NT_out = 1;
-        s.NW_out = 8;
-    } else {
-        s.NT_out = (dv % 32 == 0) ? 2 : 1;
+    // dv not a multiple of 128: the 16-column state kernel.  Output pass:
+    // 32-column waves where dv allows, as many waves (up to 4) as divide the
+    // tiles.  Map pass (dv + 128 columns): two waves per SIMD (8-wave
+    // workgroups of 32-column waves) where the tiling allows, so the waves
+    // hide each other's LDS and copy latency; otherwise wider or fewer waves.
+    s.NT_out = (dv % 32 == 0) ? 2 : 1;
+    {
         const int tiles = dv / (16 * s.NT_out);
         s.NW_out = (tiles % 4 == 0) ? 4 : (tiles % 2 == 0) ? 2 : 1;
     }
@@ -2066,7 +2037,7 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
             }
             return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: no state kernel for %d waves", NW);
         case 8:
-            if constexpr ((MODE == kModeMap && NT <= 2) || (MODE == kModeOut && NT == 1)) {
+            if constexpr (MODE == kModeMap && NT <= 2) {
                 hipLaunchKernelGGL((gdn_prefill_state_kernel<MODE, 8, NT>), grid, dim3(512), 0, stream, p, sg);
                 break;
             }
@@ -2303,7 +2274,8 @@ int gdn_prefill_state_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf
 // GPU (each device that loads this code object holds it until the process
 // ends).  Its device address is looked up once per device, with that device
 // current, on the first call there; host code uses only that address (the
-// array's own name is a host-side stand-in, not a device pointer).  Nothing in
+// array's own name is a host-side stand-in, not a device pointer); the
+// stream must belong to the current device.  Nothing in
 // the workspace has to start zeroed: every chunk slot and group map that a
 // kernel reads was written earlier in the same call.  Calls that overlap on
 // one GPU (e.g. on two streams) share the array and race.
@@ -2314,12 +2286,22 @@ constexpr size_t kScratchBytes = static_cast<size_t>(GDN_PREFILL_NOALLOC_MAX_BYT
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
-struct ScratchSlot {
-    std::once_flag once;
-    void* ptr = nullptr;
-    hipError_t err = hipSuccess;
-};
-ScratchSlot g_scratch[kMaxDevices];
+// Device address of `scratch` per device, set once a lookup has succeeded (a
+// failed lookup is not cached: the next call on that device tries again).
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// `scratch`'s address on the current device `dev`, or null with *err set.
+void* scratch_ptr(int dev, hipError_t* err) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (*err != hipSuccess) return nullptr;
+        g_scratch[dev] = ptr;
+    }
+    return g_scratch[dev];
+}
 
 }  // namespace
 
@@ -2343,12 +2325,21 @@ int gdn_prefill_noalloc_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(GDN_ERR_HIP, "prefill_noalloc: hipGetDevice failed");
     if (dev < 0 || dev >= kMaxDevices) return fail(GDN_ERR_UNSUPPORTED, "prefill_noalloc: device %d", dev);
-    ScratchSlot& s = g_scratch[dev];
-    std::call_once(s.once, [&s]() { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
-    if (s.err != hipSuccess || !s.ptr)
-        return fail(GDN_ERR_HIP, "prefill_noalloc: scratch address lookup failed: %s", hipGetErrorString(s.err));
+    // The buffer is the current device's: a stream of another device would
+    // run the kernels there against this device's address.
+    if (stream) {
+        int sdev = -1;
+        if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess)
+            return fail(GDN_ERR_HIP, "prefill_noalloc: hipStreamGetDevice failed");
+        if (sdev != dev)
+            return fail(GDN_ERR_INVALID_ARGUMENT, "prefill_noalloc: stream is on device %d, the current device is %d",
+                        sdev, dev);
+    }
+    hipError_t err = hipSuccess;
+    void* const ws = scratch_ptr(dev, &err);
+    if (!ws) return fail(GDN_ERR_HIP, "prefill_noalloc: scratch address lookup failed: %s", hipGetErrorString(err));
     return prefill_batch(q, k, v, A_log, a, dt_bias, b_logits, mask, state_in, scale, out, state_out, B, H, T, dk,
-                         dv, s.ptr, kScratchBytes, stream, 3);
+                         dv, ws, kScratchBytes, stream, 3);
 }
 
 }  // extern "C"

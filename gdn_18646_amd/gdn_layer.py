@@ -123,8 +123,11 @@ class GDNLayerCustom:
         return _zero_decode_state(self.w, B, device=device)
 
     def _decode_scratch(self, B, device):
-        """Per-(B, device) intermediates of the fused decode step, kept across steps."""
-        key = (B, str(device))
+        """Intermediates of the fused decode step, kept across steps, one set per
+        (B, device, stream): decode steps on different streams (and a graph
+        captured on its capture stream, replayed beside eager steps) do not
+        share them.  Steps of one batch size issued on one stream run in order."""
+        key = (B, str(device), torch.cuda.current_stream(device).cuda_stream)
         buf = self._scratch.get(key)
         if buf is None:
             bf = dict(dtype=torch.bfloat16, device=device)
@@ -230,6 +233,9 @@ class GDNLayerCustom:
         tokens (the reference baseline's decode semantics).  With
         ``inplace=True`` the state tensors are updated in place and the same
         dict is returned (no allocation of a new 4-D state per step).
+        The fused step (B <= 16) keeps its q/k/v/a/b/o intermediates per
+        (batch size, device, stream), so concurrent decodes of one layer must
+        run on different streams (or different batch sizes).
         """
         B, T, _ = x.shape
         assert T == 1, f"decode expects T=1, got T={T}"

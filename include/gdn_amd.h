@@ -124,6 +124,8 @@ int gdn_prefill_tm_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_
  * GDN_ERR_WORKSPACE before any HIP call (e.g. B=1, H=16, T=8192, dk=dv=128
  * needs 40 MiB and B=4, H=16, T=4096 56 MiB, which fit; B=4, H=16, T=8192
  * needs 88 MiB and does not).
+ * The buffer used is the current device's, so `stream` (when not null) must
+ * belong to the current device (else GDN_ERR_INVALID_ARGUMENT).
  * All calls on one GPU share the buffer: calls that overlap on one GPU (two
  * streams, two threads) race, so serialise them.  Nothing in it needs to
  * start zeroed.  Outputs are bit-identical to gdn_prefill_hip's.

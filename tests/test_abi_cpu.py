@@ -127,13 +127,22 @@ def test_decode_projection_validation_errors():
 
 
 def test_decode_step_validation_errors():
-    """The fused step checks each stage's arguments before that stage launches."""
+    """The fused step checks every stage's arguments before its first launch."""
     step_args = lambda B, D, dv: ([FAKE, FAKE, 1e-6] + [FAKE] * 10 + [0.1] + [FAKE] * 8 + [B, D, 2, 128, dv, 4, None])
     with pytest.raises(GdnError, match="decode_in_proj.*B=17"):
         abi.call("gdn_layer_decode_step_hip", *step_args(17, 2048, 128))
     with pytest.raises(GdnError, match="decode_in_proj.*D=100"):
         abi.call("gdn_layer_decode_step_hip", *step_args(4, 100, 128))
     abi.call("gdn_layer_decode_step_hip", *step_args(0, 2048, 128))  # B == 0: no-op
+    # Later stages are checked before the first launch too (no GPU here: a
+    # launch would fail with a HIP error instead of these messages), so a
+    # refused step leaves the conv caches and x_n history untouched.
+    with pytest.raises(GdnError, match="decode: dv=16"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(4, 2048, 16))
+    misaligned = step_args(4, 2048, 128)
+    misaligned[11] = FAKE + 4  # S_in
+    with pytest.raises(GdnError, match="decode: q/k/S/o need 16-byte"):
+        abi.call("gdn_layer_decode_step_hip", *misaligned)
 
 
 def test_binding_module_api_matches_reference():

@@ -135,3 +135,67 @@ def test_decode_conv_step_f32_vs_brute_force():
     torch.testing.assert_close(y.double(), conv * torch.sigmoid(conv), rtol=1e-2, atol=1e-3)
     assert torch.equal(new_cache[:, :, :2], cache[:, :, 1:])
     assert torch.equal(new_cache[:, :, 2], (x[:, 3].float() @ W.float().T).bfloat16())
+
+
+def _layer_f64(w, x, swap_ab=False):
+    """The layer in float64, token by token, restated from the reference's text
+    (gdn_layer.py:120-158, decode gdn_layer.py:161-200) and sharing no code with
+    oracle/layer_ref.py: RMSNorm (eps 1e-6), q/k/v = SiLU(causal depthwise conv
+    of xn W^T, taps w[c, j] on token t - (CK - 1) + j), a = xn W_a^T,
+    b = xn W_b^T, the per-token recurrence (oracle/recurrence_f64.py), then
+    y = o W_o^T.  ``swap_ab`` feeds W_b to the decay and W_a to beta: the
+    wrong wiring, which the comparison must be able to tell apart."""
+    from oracle.recurrence_f64 import gates_f64, recurrence
+    B, T, D = x.shape
+    H = w['A_log'].numel()
+    DK, DV, CK = w['W_q'].shape[0] // H, w['W_v'].shape[0] // H, w['conv_q'].shape[1]
+    x64 = x.double()
+    xn = x64 * torch.rsqrt((x64 ** 2).mean(-1, keepdim=True) + 1e-6) * w['norm_gamma'].double()
+
+    def pcs(W, cw):
+        P = xn @ W.double().T
+        Pp = torch.nn.functional.pad(P, (0, 0, CK - 1, 0))
+        c = sum(Pp[:, j:j + T] * cw.double()[:, j] for j in range(CK))
+        return c * torch.sigmoid(c)
+
+    q = pcs(w['W_q'], w['conv_q']).reshape(B, T, H, DK).permute(0, 2, 1, 3)
+    k = pcs(w['W_k'], w['conv_k']).reshape(B, T, H, DK).permute(0, 2, 1, 3)
+    v = pcs(w['W_v'], w['conv_v']).reshape(B, T, H, DV).permute(0, 2, 1, 3)
+    Wa, Wb = (w['W_b'], w['W_a']) if swap_ab else (w['W_a'], w['W_b'])
+    a = (xn @ Wa.double().T).permute(0, 2, 1)
+    b = (xn @ Wb.double().T).permute(0, 2, 1)
+    g, beta = gates_f64(w['A_log'].numpy(), a.numpy(), float(w['dt_bias']), b.numpy())
+    o, S = recurrence(q.numpy(), k.numpy(), v.numpy(), g, beta, torch.ones(B, T).numpy(), scale=DK ** -0.5)
+    o = torch.from_numpy(o).permute(0, 2, 1, 3).reshape(B, T, H * DV)
+    return o @ w['W_o'].double().T, torch.from_numpy(S)
+
+
+def _rel_err(y, y_ref):
+    y, y_ref = y.double(), y_ref.double()
+    return ((y - y_ref).norm() / y_ref.norm()).item()
+
+
+def test_layer_wiring_vs_f64_restatement():
+    """The oracle layer (forward and token-by-token decode, fp32 projections)
+    against the float64 restatement: output and final state within bf16
+    rounding (1e-2 relative), while the same restatement with W_a and W_b
+    swapped is far off -- so which weight feeds the decay, beta and the output
+    projection is pinned by something other than the layer's own decode ==
+    prefill check."""
+    w = _small_weights(D=64, H=2, DK=16, DV=8, seed=21)
+    w['A_log'] = torch.tensor([-0.5, 0.3])
+    w['dt_bias'] = torch.tensor(0.2)
+    w['norm_gamma'] = (1 + 0.2 * torch.randn(64, generator=torch.Generator().manual_seed(22))).bfloat16()
+    x = torch.randn(2, 30, 64, generator=torch.Generator().manual_seed(23)).bfloat16()
+    y64, S64 = _layer_f64(w, x)
+    layer = GDNLayerBaseline(w, chunk_size=16, fp32_proj=True)
+    y, S = layer.forward(x, return_state=True)
+    assert _rel_err(y, y64) < 1e-2 and _rel_err(S, S64) < 1e-2
+    state = layer.init_decode_state(2)
+    outs = []
+    for t in range(30):
+        y_t, state = layer.decode(x[:, t:t + 1], state)
+        outs.append(y_t)
+    assert _rel_err(torch.cat(outs, 1), y64) < 1e-2 and _rel_err(state['recurrent'], S64) < 1e-2
+    y_sw, S_sw = _layer_f64(w, x, swap_ab=True)
+    assert _rel_err(y_sw, y64) > 0.1 and _rel_err(S_sw, S64) > 0.1

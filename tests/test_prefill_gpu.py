@@ -142,14 +142,19 @@ def test_prefill_state_composition_full_size(exts, dev):
 
 
 @pytest.mark.parametrize("B,H,T,dv,masked", [(1, 1, 4000, 16, False), (1, 2, 1500, 64, True),
-                                              (2, 1, 2600, 48, True), (8, 16, 650, 128, True)])
+                                              (2, 1, 2600, 48, True), (4, 16, 650, 128, True),
+                                              (1, 16, 4096, 256, False), (1, 2, 2048, 384, True),
+                                              (1, 2, 2048, 512, False)])
 def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
     """Few (sequence, head) pairs and long sequences: the state pass splits each
-    sequence into chunk groups and joins them through the groups' affine maps
-    (2 to 13 groups here, with 16- and 32-column tiles; at 128 pairs and two
-    groups the map pass runs psi and phi in separate 16-column workgroups).  Slow
-    decay (A_log = -8, about 0.9998 per token) so the state carried into each
-    group matters: a wrong transition map would show at O(1)."""
+    sequence into chunk groups and joins them through the groups' affine maps.
+    Cases: 2 to 13 groups with the 16-column kernel (dv 16, 64, 48); the
+    32-column kernel at 64 pairs (2 groups); and the 32-column kernel with
+    several 128-column blocks per head, where the map pass runs psi in blocks
+    0 .. dv/128 - 1 and phi in the last block (dv = 256 at the reference's
+    H = 16: 8 groups; dv = 384 and 512 at H = 2: 8 groups).  Slow decay
+    (A_log = -8, about 0.9998 per token) so the state carried into each group
+    matters: a wrong transition map would show at O(1)."""
     d = synth.prefill_inputs(B, T, H, 128, dv, seed=T + dv, state=True)
     d["A_log"] = torch.linspace(-8.0, -2.0, H)
     mask = None
@@ -224,6 +229,24 @@ def test_prefill_varlen_group_cap_binds(exts, dev, dv):
     lengths = [6400, 100]
     d = synth.varlen_inputs(lengths, 2, 128, dv, seed=13)
     d["A_log"] = torch.tensor([-6.0, -2.0])
+    g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+    out, S = exts["prefill"].prefill_varlen(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"],
+                                            d["cu_seqlens"], g["state_in"], 0.0)
+    torch.cuda.synchronize()
+    o_ref, S_ref = ref_prefill_varlen(d["q"], d["k"], d["v"], d["A_log"], d["a"], 0.0, d["b_logits"],
+                                      d["cu_seqlens"], state_in=d["state_in"], chunk_size=64)
+    assert_out_close(out.cpu(), o_ref)
+    for i in range(len(lengths)):
+        assert_state_close(S[i].cpu(), S_ref[i], what=f"state of sequence {i}")
+
+
+def test_prefill_varlen_chunk_groups_dv256(exts, dev):
+    """Packed sequences at dv = 256 (two 128-column blocks a head, psi in
+    both, phi in a third) with chunk groups planned per sequence: at H = 4
+    the plan targets 32 slots a head for lengths 4000, 900, 2500."""
+    lengths = [4000, 900, 2500]
+    d = synth.varlen_inputs(lengths, 4, 128, 256, seed=17)
+    d["A_log"] = torch.tensor([-8.0, -5.0, -3.0, -1.0])
     g = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
     out, S = exts["prefill"].prefill_varlen(g["q"], g["k"], g["v"], g["A_log"], g["a"], 0.0, g["b_logits"],
                                             d["cu_seqlens"], g["state_in"], 0.0)
