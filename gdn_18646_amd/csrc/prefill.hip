@@ -1146,9 +1146,12 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 // rows and columns are zero (beta m = 0 there), so they add exact zeros.
 constexpr int kObPitch = 272;                // output tile row pitch (bytes)
 constexpr int kObBytes = kC * kObPitch;      // one output tile
-template <int MODE>
+template <int MODE, int NCW = 4>
 struct Stage4 {
+    static_assert(NCW == 4 || (NCW == 2 && MODE == kModeOut), "compute waves per workgroup");
     static constexpr bool out = MODE == kModeOut;
+    static constexpr int ncw = NCW;        // compute waves (32 state columns each)
+    static constexpr int cols = 32 * NCW;  // state columns of a workgroup
     static constexpr int offK = 0;
     static constexpr int offQ = 16 * kFragB;
     static constexpr int offR = offQ + (out ? 16 : 0) * kFragB;
@@ -1159,12 +1162,12 @@ struct Stage4 {
     static constexpr int offH = offR + kRecH * kFragB;
     static constexpr int offAq = offR + nRec * kFragB;  // output pass: Aq, formed by the copy waves
     static constexpr int offV = offAq + (out ? 6 : 0) * kFragB;
-    static constexpr int bytes = offV + 16 * kFragB;
+    static constexpr int bytes = offV + 4 * NCW * kFragB;
     static constexpr int ob_bytes = out ? kObBytes : 0;
-    // waves: 4 compute, then (output pass) 2 copying chunks in, a store wave
+    // waves: NCW compute, then (output pass) 2 copying chunks in, a store wave
     // and the Aq wave
     static constexpr int loaders = out ? 2 : 0;
-    static constexpr int nWaves = 4 + loaders + (out ? 2 : 0);
+    static constexpr int nWaves = NCW + loaders + (out ? 2 : 0);
     static constexpr int nStores = out ? kC * 256 / kFragB : 0;  // output store instructions per chunk
 };
 
@@ -1178,10 +1181,10 @@ struct Lane4 {
 // map pass each compute wave takes a quarter, STRIDE 4).  `row0`: q/k/v row
 // of the chunk's first token; `rec`: the chunk's record; `vcol0`: the
 // workgroup's first V column.
-template <int MODE, bool FULL, int STRIDE>
+template <int MODE, int NCW, bool FULL, int STRIDE>
 __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf, size_t row0, const u32x4* rec,
                                              int vcol0, int nvalid, int first, int lane, const Lane4& L, bool v_on) {
-    using St = Stage4<MODE>;
+    using St = Stage4<MODE, NCW>;
     // Full chunks: uniform bases, fixed lane offsets.  The partial chunk:
     // base at the chunk's first row and each lane's row clamped to the
     // sequence, so every offset is non-negative and in range.
@@ -1221,7 +1224,7 @@ __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf
     if (v_on) {  // job u: compute wave u / 4's columns, rows 16 (u % 4) ..
         const unsigned char* vb = reinterpret_cast<const unsigned char*>(p.v + row0 * p.dv + vcol0);
 #pragma unroll
-        for (int i = 0; i < 16 / STRIDE; ++i) {
+        for (int i = 0; i < 4 * NCW / STRIDE; ++i) {
             const int u = first + STRIDE * i, w = u >> 2, it = u & 3;
             lds_u8* vd = buf + St::offV + u * kFragB;
             if (FULL) {
@@ -1285,17 +1288,21 @@ __device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
 }
 
 // The copy wave: chunk c's output tile from LDS to `ob` (row 0, the
-// workgroup's first column), 4 rows of 256 bytes per instruction.
-template <bool FULL>
+// workgroup's first column), rows of RB bytes (the workgroup's columns): 4
+// rows of 256 bytes or 8 rows of 128 bytes per instruction.
+template <bool FULL, int RB>
 __device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, int orow, int nvalid, int lane) {
-    // Opaque per call: otherwise the 16 per-lane row offsets are hoisted out
-    // of the chunk loop and held in registers that every wave then pays for.
+    constexpr int LPR = RB / 16;  // lanes per row
+    static_assert(LPR == 16 || LPR == 8, "output row bytes");
+    // Opaque per call: otherwise the per-lane row offsets are hoisted out of
+    // the chunk loop and held in registers that every wave then pays for.
     asm volatile("" : "+s"(orow));
 #pragma unroll
-    for (int i = 0; i < kC / 4; ++i) {
-        const int row = 4 * i + (lane >> 4);
-        const u32x4 v = *reinterpret_cast<const lds_u32x4*>(obuf + row * kObPitch + (lane & 15) * 16);
-        if (FULL || row < nvalid) *reinterpret_cast<u32x4*>(ob + static_cast<size_t>(row) * orow + (lane & 15) * 8) = v;
+    for (int i = 0; i < kC * LPR / 64; ++i) {
+        const int row = (64 / LPR) * i + lane / LPR;
+        const u32x4 v = *reinterpret_cast<const lds_u32x4*>(obuf + row * kObPitch + (lane % LPR) * 16);
+        if (FULL || row < nvalid)
+            *reinterpret_cast<u32x4*>(ob + static_cast<size_t>(row) * orow + (lane % LPR) * 8) = v;
     }
 }
 
@@ -1481,10 +1488,12 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 // The output pass adds the copy waves.  In the map pass (two workgroups per
 // CU, 39 KiB a chunk step each) the compute waves issue a quarter of the
 // copies each: dedicated copy waves there measured slower.
-template <int MODE>
-__global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_waves_per_eu(
+template <int MODE, int NCW>
+__global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((amdgpu_waves_per_eu(
     MODE == kModeOut ? 1 : 2, 2))) void gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
-    using St = Stage4<MODE>;
+    using St = Stage4<MODE, NCW>;
+    // state4_step reads the operands at the offsets of the 4-wave layout.
+    static_assert(St::offV == Stage4<MODE>::offV && St::offAq == Stage4<MODE>::offAq, "stage layout");
     constexpr bool OUT = St::out;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * St::bytes + 2 * St::ob_bytes];
     auto buf = [&](int i) { return (lds_u8*)&smem[0] + i * St::bytes; };
@@ -1521,18 +1530,18 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
     // Copy waves (output pass): 4 and 5 copy chunk c + 1 in, 6 writes chunk
     // c - 1's outputs, 7 forms chunk c's Aq.  In the map pass the compute
     // waves copy (`issuer`).
-    const bool loader = OUT && wave >= 4 && wave < 4 + St::loaders;
-    const bool storer = OUT && wave == 4 + St::loaders;
-    const bool aqw = OUT && wave == 5 + St::loaders;
+    const bool loader = OUT && wave >= NCW && wave < NCW + St::loaders;
+    const bool storer = OUT && wave == NCW + St::loaders;
+    const bool aqw = OUT && wave == NCW + 1 + St::loaders;
     const bool issuer = OUT ? loader : true;
     const bool copier = loader || storer || aqw;
     const int cw = copier ? 0 : wave;  // compute wave (column block)
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
     const int dv = p.dv;
-    const int col0_wave = vg * 128 + 32 * cw;  // map pass: >= dv means identity columns
-    const bool phi_cols = MODE == kModeMap && vg * 128 >= dv;
-    const int vcol0 = phi_cols ? 0 : vg * 128;
+    const int col0_wave = vg * St::cols + 32 * cw;  // map pass: >= dv means identity columns
+    const bool phi_cols = MODE == kModeMap && vg * St::cols >= dv;
+    const int vcol0 = phi_cols ? 0 : vg * St::cols;
     const int nchunks = (sq.len + kC - 1) / kC;
     const int glen = (nchunks + ngroups - 1) / ngroups;
     const int c_begin = min(grp * glen, nchunks), c_end = min(c_begin + glen, nchunks);
@@ -1546,7 +1555,7 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
     auto rows = [&](int c) { return head_row0 + static_cast<size_t>(c) * kC; };
     auto obase = [&](int c) {  // out row of chunk c's first token, the workgroup's first column
         const size_t tok = static_cast<size_t>(sq.b) * p.T_stride + sq.tok0 + static_cast<size_t>(c) * kC;
-        return p.out + (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + vg * 128;
+        return p.out + (p.out_tm ? (tok * p.H + h) * dv : rows(c) * dv) + vg * St::cols;
     };
     auto nval = [&](int c) { return min(kC, sq.len - c * kC); };
     auto rec = [&](int c) { return p.wsR + (static_cast<size_t>(sq.slot0 + c) * p.H + h) * kRecShort * 64; };
@@ -1554,14 +1563,14 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
         // Opaque per call: otherwise the copies' LDS addresses (buffer and
         // fragment constants) are hoisted out of the chunk loop and held in
         // SGPRs, which runs the kernel out of them.
-        int first = OUT ? wave - 4 : wave;
+        int first = OUT ? wave - NCW : wave;
         asm volatile("" : "+s"(first));
         lds_u8* b = buf(bi);
         constexpr int STRIDE = OUT ? St::loaders : 4;
         if (nval(c) == kC)
-            stage4_issue<MODE, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
+            stage4_issue<MODE, NCW, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
         else
-            stage4_issue<MODE, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
+            stage4_issue<MODE, NCW, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
     };
 
     // Chunk c = c_begin + k uses buffer k % 2 and output tile k % 2.  Barrier
@@ -1581,16 +1590,16 @@ __global__ __launch_bounds__(64 * Stage4<MODE>::nWaves) __attribute__((amdgpu_wa
                 if (loader && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
                 if (aqw) stage4_aq(buf(k & 1), lane);
                 // Chunk c - 1 is never a sequence's partial last chunk here.
-                if (storer && k >= 1) stage4_store<true>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
+                if (storer && k >= 1) stage4_store<true, 2 * St::cols>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
                 lds_barrier();  // chunk c's Aq formed
             }
             lds_barrier();  // the last chunk's outputs are in LDS
             if (storer && c_end > c_begin) {
                 const int c = c_end - 1, k = c - c_begin;
                 if (nval(c) == kC)
-                    stage4_store<true>(obuf(k & 1), obase(c), orow, kC, lane);
+                    stage4_store<true, 2 * St::cols>(obuf(k & 1), obase(c), orow, kC, lane);
                 else
-                    stage4_store<false>(obuf(k & 1), obase(c), orow, nval(c), lane);
+                    stage4_store<false, 2 * St::cols>(obuf(k & 1), obase(c), orow, nval(c), lane);
             }
             return;
         }
@@ -1902,6 +1911,7 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 struct StatePlan {
     int NT_out, NW_out, nvg_out, NT_map, NW_map, nvg_map, G;
     bool wide;  // dv % 128 == 0: gdn_prefill_state4_kernel (4 waves x 32 columns, 128 columns a workgroup)
+    bool half;  // wide, output pass in 64-column workgroups (2 compute waves): one group, few pairs
 };
 
 // `exact`: max_chunks is the exact chunk count of every sequence, so the
@@ -1911,6 +1921,7 @@ struct StatePlan {
 StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact, bool varlen) {
     StatePlan s;
     s.wide = dv % 128 == 0;
+    s.half = false;
     if (s.wide) {
         s.NT_out = s.NT_map = 2;
         s.NW_out = s.NW_map = 4;
@@ -1928,6 +1939,12 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact,
             G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
         if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
         s.G = G < 2 ? 1 : static_cast<int>(G);
+        // One group and at most half the CUs busy: split each head's 128
+        // columns over two workgroups of two compute waves (the state columns
+        // update independently; the halves of a head share K and Q through
+        // the L2 of their XCD).
+        s.half = s.G == 1 && base <= 128;
+        if (s.half) s.nvg_out = dv / 64;
         return s;
     }
     // dv not a multiple of 128: the 16-column state kernel.  Output pass:
@@ -2009,12 +2026,12 @@ int check_common(const char* who, int H, int dk, int dv) {
     return GDN_OK;
 }
 
-template <int MODE>
+template <int MODE, int NCW>
 int launch_state4(const PrefillParams& p, const StateGrid& sg, hipStream_t stream) {
     const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups_run * sg.nvg;
     if (nwg > 0x7fffffffLL) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE>), dim3(static_cast<unsigned>(nwg)), dim3(64 * Stage4<MODE>::nWaves),
-                       0, stream, p, sg);
+    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE, NCW>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(64 * Stage4<MODE, NCW>::nWaves), 0, stream, p, sg);
     return gdn_host::check_launch(MODE == kModeMap ? "gdn_prefill_state4_kernel<map>" : "gdn_prefill_state4_kernel");
 }
 
@@ -2050,7 +2067,11 @@ int launch_state(const PrefillParams& p, const StateGrid& sg, int NW, hipStream_
 
 template <int MODE>
 int launch_state_plan(const PrefillParams& p, const StateGrid& sg, const StatePlan& sp, hipStream_t stream) {
-    if (sp.wide) return launch_state4<MODE>(p, sg, stream);
+    if (sp.wide) {
+        if constexpr (MODE == kModeOut)
+            if (sp.half) return launch_state4<MODE, 2>(p, sg, stream);
+        return launch_state4<MODE, 4>(p, sg, stream);
+    }
     if (MODE == kModeMap)
         return sp.NT_map == 4   ? launch_state<MODE, 4>(p, sg, sp.NW_map, stream)
                : sp.NT_map == 2 ? launch_state<MODE, 2>(p, sg, sp.NW_map, stream)

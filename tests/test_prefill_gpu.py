@@ -168,6 +168,25 @@ def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
     assert_state_close(S, S_ref)
 
 
+@pytest.mark.parametrize("B,H,T,dv,masked", [(8, 16, 1000, 128, True), (4, 16, 700, 256, False),
+                                              (8, 16, 8192, 128, False)])
+def test_prefill_half_width_output_pass(exts, dev, B, H, T, dv, masked):
+    """At most 128 (sequence, head) pairs and one chunk group: the output pass
+    splits each head's columns over workgroups of 64 (two compute waves), so
+    B=8, H=16 runs 256 workgroups.  Nonzero initial states, a ragged last
+    chunk, masked tokens, dv = 256 (four workgroups a head), and the B=8
+    T=8192 bench shape."""
+    d = synth.prefill_inputs(B, T, H, 128, dv, seed=B * T + dv, state=True)
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(T)
+        mask = (torch.rand(B, T, generator=g) > 0.1).float()
+    out, S = _kernel(exts, d, dev, mask=mask, state_in=d["state_in"])
+    o_ref, S_ref = _oracle(d, mask=mask, state_in=d["state_in"])
+    assert_out_close(out, o_ref)
+    assert_state_close(S, S_ref)
+
+
 @pytest.mark.parametrize("B,H,T,dv", [(1, 16, 8192, 128), (2, 3, 130, 128), (1, 2, 1500, 64), (3, 5, 100, 48),
                                        (2, 4, 257, 256)])
 def test_prefill_token_major_output(exts, dev, B, H, T, dv):
