@@ -1751,9 +1751,15 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
     } else {
         S = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // psi/phi unit of group j: unit0 + j ustride (group_unit, with the plan
+    // table read once here: a table read inside the step loop would come with
+    // a wait for every load in flight, the prefetched steps included).
+    const size_t unit0 = PLANNED ? static_cast<size_t>(plan_first(sg, sidx)) * p.H + h
+                                 : static_cast<size_t>(sidx * p.H + h) * sg.ngroups;
+    const size_t ustride = PLANNED ? static_cast<size_t>(p.H) : 1;
+    auto unit = [&](int j) { return unit0 + static_cast<size_t>(j) * ustride; };
     auto psi_at = [&](int j) {
-        return reinterpret_cast<f32x4*>(sg.psi + (group_unit(sg, p.H, sidx, h, j) * ntile + tile) * 2048) +
-               wave * 64 + lane;
+        return reinterpret_cast<f32x4*>(sg.psi + (unit(j) * ntile + tile) * 2048) + wave * 64 + lane;
     };
     // This wave's phi fragments (row tile r, k-steps 0..3: 4 contiguous KiB)
     // and psi quad r of step j, into register slot j % kScanDepth.
@@ -1761,8 +1767,7 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
     u32x4 ph[D][4];
     f32x4 ps[D];
     auto load = [&](int j) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(sg.phi + group_unit(sg, p.H, sidx, h, j) * kDK * kDK) +
-                           4 * wave * 64 + lane;
+        const u32x4* src = reinterpret_cast<const u32x4*>(sg.phi + unit(j) * kDK * kDK) + 4 * wave * 64 + lane;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) ph[j % D][ks] = src[ks * 64];
         ps[j % D] = *psi_at(j);
