@@ -1146,12 +1146,11 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 // rows and columns are zero (beta m = 0 there), so they add exact zeros.
 constexpr int kObPitch = 272;                // output tile row pitch (bytes)
 constexpr int kObBytes = kC * kObPitch;      // one output tile
-template <int MODE, int NCW = 4>
+template <int MODE, int NT = 2>
 struct Stage4 {
-    static_assert(NCW == 4 || (NCW == 2 && MODE == kModeOut), "compute waves per workgroup");
+    static_assert(NT == 2 || (NT == 1 && MODE == kModeOut), "16-column tiles per compute wave");
     static constexpr bool out = MODE == kModeOut;
-    static constexpr int ncw = NCW;        // compute waves (32 state columns each)
-    static constexpr int cols = 32 * NCW;  // state columns of a workgroup
+    static constexpr int cols = 64 * NT;  // state columns of a workgroup (4 compute waves x 16 NT)
     static constexpr int offK = 0;
     static constexpr int offQ = 16 * kFragB;
     static constexpr int offR = offQ + (out ? 16 : 0) * kFragB;
@@ -1162,12 +1161,12 @@ struct Stage4 {
     static constexpr int offH = offR + kRecH * kFragB;
     static constexpr int offAq = offR + nRec * kFragB;  // output pass: Aq, formed by the copy waves
     static constexpr int offV = offAq + (out ? 6 : 0) * kFragB;
-    static constexpr int bytes = offV + 4 * NCW * kFragB;
+    static constexpr int bytes = offV + 8 * NT * kFragB;  // V: [64 rows][32 columns] per 32 columns
     static constexpr int ob_bytes = out ? kObBytes : 0;
-    // waves: NCW compute, then (output pass) 2 copying chunks in, a store wave
+    // waves: 4 compute, then (output pass) 2 copying chunks in, a store wave
     // and the Aq wave
     static constexpr int loaders = out ? 2 : 0;
-    static constexpr int nWaves = NCW + loaders + (out ? 2 : 0);
+    static constexpr int nWaves = 4 + loaders + (out ? 2 : 0);
     static constexpr int nStores = out ? kC * 256 / kFragB : 0;  // output store instructions per chunk
 };
 
@@ -1181,10 +1180,10 @@ struct Lane4 {
 // map pass each compute wave takes a quarter, STRIDE 4).  `row0`: q/k/v row
 // of the chunk's first token; `rec`: the chunk's record; `vcol0`: the
 // workgroup's first V column.
-template <int MODE, int NCW, bool FULL, int STRIDE>
+template <int MODE, int NT, bool FULL, int STRIDE>
 __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf, size_t row0, const u32x4* rec,
                                              int vcol0, int nvalid, int first, int lane, const Lane4& L, bool v_on) {
-    using St = Stage4<MODE, NCW>;
+    using St = Stage4<MODE, NT>;
     // Full chunks: uniform bases, fixed lane offsets.  The partial chunk:
     // base at the chunk's first row and each lane's row clamped to the
     // sequence, so every offset is non-negative and in range.
@@ -1224,7 +1223,7 @@ __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf
     if (v_on) {  // job u: compute wave u / 4's columns, rows 16 (u % 4) ..
         const unsigned char* vb = reinterpret_cast<const unsigned char*>(p.v + row0 * p.dv + vcol0);
 #pragma unroll
-        for (int i = 0; i < 4 * NCW / STRIDE; ++i) {
+        for (int i = 0; i < 8 * NT / STRIDE; ++i) {
             const int u = first + STRIDE * i, w = u >> 2, it = u & 3;
             lds_u8* vd = buf + St::offV + u * kFragB;
             if (FULL) {
@@ -1316,14 +1315,18 @@ __device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, i
 // (PHASE()) keep that order: the scheduler would otherwise sink reads to
 // their first use (exposing the LDS latency at every one) or hoist all of
 // them to the top (past the 256 VGPRs a wave has).
-template <int MODE, typename Mid>
-__device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2], lds_u8* obuf, int wave, int lane,
+template <int MODE, int NT, typename Mid>
+__device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][NT], lds_u8* obuf, int wave, int lane,
                                             bool v_zero, uint32_t kt_lane, Mid mid) {
-    using St = Stage4<MODE>;
+    using St = Stage4<MODE, NT>;
     constexpr bool OUT = St::out;
     const int n = lane & 15, g = lane >> 4;
     const lds_f32* G = reinterpret_cast<const lds_f32*>(buf + St::offG);
-    const lds_u8* Vs = buf + St::offV + wave * 4 * kFragB;
+    // V is staged per 32 columns ([64 rows][32 columns]): a 32-column wave
+    // reads its own tile, two 16-column waves share one (wave 2 i + 1 takes
+    // its upper 16 columns).
+    const lds_u8* Vs = buf + St::offV + (NT == 2 ? wave : wave >> 1) * 4 * kFragB;
+    const int vnt0 = NT == 2 ? 0 : (wave & 1);
 #define PHASE() __builtin_amdgcn_sched_barrier(0)
 
     // (a) X = K S and P^T = S^T Q^T.  The state's bf16 copy is the B operand
@@ -1337,7 +1340,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
             if constexpr (OUT) qf[slot][mt] = frag(buf, St::offQ + (4 * mt + s) * kFragB, lane);
         }
     };
-    i16x4 vv[2][4];
+    i16x4 vv[NT][4];
     f32x4 gam[4], kd[4];
     float gC = 0.f;
     // (b)'s operands: V in the accumulator layout (column n, rows
@@ -1346,12 +1349,12 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
     auto load_b = [&]() {
         const lds_u8* vrow = Vs + ((4 * g + ((lane >> 2) & 3)) * 32 + 4 * (lane & 3)) * 2;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
                 vv[nt][mt] = v_zero ? i16x4{0, 0, 0, 0}
                                     : __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                          (lds_i16x4*)(vrow + (16 * mt * 32 + 16 * nt) * 2));
+                                          (lds_i16x4*)(vrow + (16 * mt * 32 + 16 * (nt + vnt0)) * 2));
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             gam[mt] = *reinterpret_cast<const lds_f32x4*>(G + 16 * mt + 4 * g);
@@ -1359,11 +1362,11 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
         }
         gC = G[kC - 1];
     };
-    f32x4 X[4][2], P[4][2];
+    f32x4 X[4][NT], P[4][NT];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; ++nt) X[mt][nt] = P[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     load_a(0, 0);
     PHASE();
 #pragma unroll
@@ -1372,13 +1375,13 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
             load_a(s + 1, (s + 1) & 1);
         else
             load_b();
-        bf16x8 Bs[2];
+        bf16x8 Bs[NT];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
+        for (int nt = 0; nt < NT; ++nt) Bs[nt] = pack8(S[2 * s][nt], S[2 * s + 1][nt]);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < NT; ++nt) {
                 X[mt][nt] = mfma16x16x32(kf[s & 1][mt], Bs[nt], X[mt][nt]);
                 if constexpr (OUT) P[mt][nt] = mfma16x16x32(Bs[nt], qf[s & 1][mt], P[mt][nt]);
             }
@@ -1391,15 +1394,15 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 X[mt][nt][i] = bf2f(static_cast<uint16_t>(vv[nt][mt][i])) - gam[mt][i] * X[mt][nt][i];
-    bf16x8 BY[2][2];
+    bf16x8 BY[2][NT];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) BY[s][nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
+        for (int nt = 0; nt < NT; ++nt) BY[s][nt] = pack8(X[2 * s][nt], X[2 * s + 1][nt]);
     PHASE();
     // (c) dV = Tp Y (Tp lower triangular: six nonzero fragments), while the
     //     first half of K^T is read.
@@ -1412,26 +1415,26 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
         }
     };
     load_kt(0);
-    f32x4 D[4][2];
+    f32x4 D[4][NT];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; ++nt) D[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int mt = 2 * s; mt < 4; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[s][nt], D[mt][nt]);
+            for (int nt = 0; nt < NT; ++nt) D[mt][nt] = mfma16x16x32(tf[aq_index(mt, s)], BY[s][nt], D[mt][nt]);
     PHASE();
     // (d) S <- gamma_C S + K^T ((gamma_C / gamma) o dV) in two halves of
     //     row tiles: the second half of K^T is read during the first, Aq
     //     during the second.
     bf16x8 af[OUT ? 6 : 1];
     float co[4];
-    bf16x8 BS0[2], BS1[2];
+    bf16x8 BS0[NT], BS1[NT];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         BS0[nt] = pack8(kd[0] * D[0][nt], kd[1] * D[1][nt]);
         BS1[nt] = pack8(kd[2] * D[2][nt], kd[3] * D[3][nt]);
     }
@@ -1449,7 +1452,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 #pragma unroll
         for (int r = 4 * half; r < 4 * half + 4; ++r)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < NT; ++nt) {
                 S[r][nt] *= gC;
                 S[r][nt] = mfma16x16x32(ktf[r][0], BS0[nt], S[r][nt]);
                 S[r][nt] = mfma16x16x32(ktf[r][1], BS1[nt], S[r][nt]);
@@ -1461,7 +1464,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
     //     output tile as 8 bytes.
     if constexpr (OUT) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const bf16x8 BD0 = pack8(D[0][nt], D[1][nt]), BD1 = pack8(D[2][nt], D[3][nt]);
             f32x4 O[4];
             O[0] = mfma16x16x32(BD0, af[0], co[0] * P[0][nt]);
@@ -1470,7 +1473,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
             O[3] = mfma16x16x32(BD1, af[5], mfma16x16x32(BD0, af[4], co[3] * P[3][nt]));
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
-                *reinterpret_cast<lds_u32x2*>(obuf + (16 * mt + n) * kObPitch + (32 * wave + 16 * nt + 4 * g) * 2) =
+                *reinterpret_cast<lds_u32x2*>(obuf + (16 * mt + n) * kObPitch + (16 * NT * wave + 16 * nt + 4 * g) * 2) =
                     pack4_bf16(O[mt]);
         }
     }
@@ -1488,12 +1491,10 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][2],
 // The output pass adds the copy waves.  In the map pass (two workgroups per
 // CU, 39 KiB a chunk step each) the compute waves issue a quarter of the
 // copies each: dedicated copy waves there measured slower.
-template <int MODE, int NCW>
-__global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((amdgpu_waves_per_eu(
+template <int MODE, int NT>
+__global__ __launch_bounds__((64 * Stage4<MODE, NT>::nWaves)) __attribute__((amdgpu_waves_per_eu(
     MODE == kModeOut ? 1 : 2, 2))) void gdn_prefill_state4_kernel(PrefillParams p, StateGrid sg) {
-    using St = Stage4<MODE, NCW>;
-    // state4_step reads the operands at the offsets of the 4-wave layout.
-    static_assert(St::offV == Stage4<MODE>::offV && St::offAq == Stage4<MODE>::offAq, "stage layout");
+    using St = Stage4<MODE, NT>;
     constexpr bool OUT = St::out;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * St::bytes + 2 * St::ob_bytes];
     auto buf = [&](int i) { return (lds_u8*)&smem[0] + i * St::bytes; };
@@ -1530,16 +1531,16 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
     // Copy waves (output pass): 4 and 5 copy chunk c + 1 in, 6 writes chunk
     // c - 1's outputs, 7 forms chunk c's Aq.  In the map pass the compute
     // waves copy (`issuer`).
-    const bool loader = OUT && wave >= NCW && wave < NCW + St::loaders;
-    const bool storer = OUT && wave == NCW + St::loaders;
-    const bool aqw = OUT && wave == NCW + 1 + St::loaders;
+    const bool loader = OUT && wave >= 4 && wave < 4 + St::loaders;
+    const bool storer = OUT && wave == 4 + St::loaders;
+    const bool aqw = OUT && wave == 5 + St::loaders;
     const bool issuer = OUT ? loader : true;
     const bool copier = loader || storer || aqw;
     const int cw = copier ? 0 : wave;  // compute wave (column block)
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
     const int dv = p.dv;
-    const int col0_wave = vg * St::cols + 32 * cw;  // map pass: >= dv means identity columns
+    const int col0_wave = vg * St::cols + 16 * NT * cw;  // map pass: >= dv means identity columns
     const bool phi_cols = MODE == kModeMap && vg * St::cols >= dv;
     const int vcol0 = phi_cols ? 0 : vg * St::cols;
     const int nchunks = (sq.len + kC - 1) / kC;
@@ -1563,14 +1564,14 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
         // Opaque per call: otherwise the copies' LDS addresses (buffer and
         // fragment constants) are hoisted out of the chunk loop and held in
         // SGPRs, which runs the kernel out of them.
-        int first = OUT ? wave - NCW : wave;
+        int first = OUT ? wave - 4 : wave;
         asm volatile("" : "+s"(first));
         lds_u8* b = buf(bi);
         constexpr int STRIDE = OUT ? St::loaders : 4;
         if (nval(c) == kC)
-            stage4_issue<MODE, NCW, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
+            stage4_issue<MODE, NT, true, STRIDE>(p, b, rows(c), rec(c), vcol0, kC, first, lane, L, !phi_cols);
         else
-            stage4_issue<MODE, NCW, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
+            stage4_issue<MODE, NT, false, STRIDE>(p, b, rows(c), rec(c), vcol0, nval(c), first, lane, L, !phi_cols);
     };
 
     // Chunk c = c_begin + k uses buffer k % 2 and output tile k % 2.  Barrier
@@ -1606,18 +1607,18 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
     }
 
     // State tile: S[r][nt][i] = S[rho(r, g, i)][col0_wave + 16 nt + n].
-    f32x4 S[8][2];
+    f32x4 S[8][NT];
     if constexpr (MODE == kModeMap) {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     S[r][nt][i] = (phi_cols && rho_row(r, g, i) == col0_wave - dv + 16 * nt + n) ? 1.f : 0.f;
     } else if (grp > 0) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const f32x4* Ps = reinterpret_cast<const f32x4*>(
                 sg.psi + (group_unit(sg, p.H, sidx, h, grp - 1) * (dv / 16) + col0_wave / 16 + nt) * 2048);
 #pragma unroll
@@ -1628,14 +1629,14 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) S[r][nt][i] = sin[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n];
     } else {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < NT; ++nt) S[r][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     if (!OUT && c_begin < c_end) issue(c_begin, 0);
@@ -1644,7 +1645,7 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
         if (!OUT) wait_vm<0>();  // chunk c staged (the map pass's compute waves copy)
         lds_barrier();
         if (!OUT && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
-        state4_step<MODE>(buf(k & 1), S, obuf(k & 1), cw, lane, phi_cols, kt_lane, [] { lds_barrier(); });
+        state4_step<MODE, NT>(buf(k & 1), S, obuf(k & 1), cw, lane, phi_cols, kt_lane, [] { lds_barrier(); });
     }
 
     if constexpr (OUT) {
@@ -1654,7 +1655,7 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) so[rho_row(r, g, i) * dv + col0_wave + 16 * nt + n] = S[r][nt][i];
     } else if (phi_cols) {
@@ -1666,7 +1667,7 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < NT; ++nt) {
                 const int T = (col0_wave - dv) / 16 + nt;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) tt[(4 * g + i) * 16 + n] = f2bf_bits(S[r][nt][i]);
@@ -1678,7 +1679,7 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NCW>::nWaves)) __attribute__((am
             }
     } else {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             f32x4* Ps = reinterpret_cast<f32x4*>(sg.psi +
                                                  (group_unit(sg, p.H, sidx, h, grp) * (dv / 16) + col0_wave / 16 + nt) * 2048);
 #pragma unroll
@@ -1916,7 +1917,7 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 struct StatePlan {
     int NT_out, NW_out, nvg_out, NT_map, NW_map, nvg_map, G;
     bool wide;  // dv % 128 == 0: gdn_prefill_state4_kernel (4 waves x 32 columns, 128 columns a workgroup)
-    bool half;  // wide, output pass in 64-column workgroups (2 compute waves): one group, few pairs
+    bool half;  // wide, output pass in 64-column workgroups (4 compute waves x 16): one group, few pairs
 };
 
 // `exact`: max_chunks is the exact chunk count of every sequence, so the
@@ -1945,9 +1946,10 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact,
         if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
         s.G = G < 2 ? 1 : static_cast<int>(G);
         // One group and at most half the CUs busy: split each head's 128
-        // columns over two workgroups of two compute waves (the state columns
-        // update independently; the halves of a head share K and Q through
-        // the L2 of their XCD).
+        // columns over two workgroups of four 16-column compute waves (the
+        // state columns update independently; the halves of a head share K
+        // and Q through the L2 of their XCD, and each wave's chain of
+        // dependent products per chunk is half as long).
         s.half = s.G == 1 && base <= 128;
         if (s.half) s.nvg_out = dv / 64;
         return s;
@@ -2031,12 +2033,12 @@ int check_common(const char* who, int H, int dk, int dv) {
     return GDN_OK;
 }
 
-template <int MODE, int NCW>
+template <int MODE, int NT>
 int launch_state4(const PrefillParams& p, const StateGrid& sg, hipStream_t stream) {
     const long long nwg = static_cast<long long>(sg.nheads) * sg.ngroups_run * sg.nvg;
     if (nwg > 0x7fffffffLL) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "prefill: grid too large");
-    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE, NCW>), dim3(static_cast<unsigned>(nwg)),
-                       dim3(64 * Stage4<MODE, NCW>::nWaves), 0, stream, p, sg);
+    hipLaunchKernelGGL((gdn_prefill_state4_kernel<MODE, NT>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(64 * Stage4<MODE, NT>::nWaves), 0, stream, p, sg);
     return gdn_host::check_launch(MODE == kModeMap ? "gdn_prefill_state4_kernel<map>" : "gdn_prefill_state4_kernel");
 }
 
@@ -2074,8 +2076,8 @@ template <int MODE>
 int launch_state_plan(const PrefillParams& p, const StateGrid& sg, const StatePlan& sp, hipStream_t stream) {
     if (sp.wide) {
         if constexpr (MODE == kModeOut)
-            if (sp.half) return launch_state4<MODE, 2>(p, sg, stream);
-        return launch_state4<MODE, 4>(p, sg, stream);
+            if (sp.half) return launch_state4<MODE, 1>(p, sg, stream);
+        return launch_state4<MODE, 2>(p, sg, stream);
     }
     if (MODE == kModeMap)
         return sp.NT_map == 4   ? launch_state<MODE, 4>(p, sg, sp.NW_map, stream)
