@@ -24,12 +24,14 @@ same-run parity of the GPU results against that oracle:
 * ``layer_e2e``: config 5, the whole layer (RMSNorm, fused projection + conv
   + SiLU, prefill, output projection) at B=4 x T=4096, then decode steps at
   B=4 continuing from the prefill state.
+* ``layer_packed``: the layer forward over config 4's 8 packed sequences at
+  config-5 dims (one packed in-projection launch, the packed prefill, W_o).
 * ``layer_decode_batches``: the layer's decode step at config-5 dims for
   B = 1, 8, 32, 64, 128, 256 (the reference's serving sweep), HBM roofline
   per B, parity against the oracle layer at B=256.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--no-extra] [--only prefill,cfg2,batches,varlen,decode,layer,serve]
+                    [--no-extra] [--only prefill,cfg2,batches,varlen,decode,layer,packed,serve]
 """
 
 import argparse
@@ -59,7 +61,7 @@ def decode_bytes(B, H):
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-LEGS = ("prefill", "cfg2", "batches", "varlen", "decode", "layer", "serve")
+LEGS = ("prefill", "cfg2", "batches", "varlen", "decode", "layer", "packed", "serve")
 
 
 def measured_traffic(kernel):
@@ -127,6 +129,44 @@ def roofline_fracs(flop, nbytes, ms):
     tf = flop / (ms / 1e3) / 1e12
     gbs = nbytes / (ms / 1e3) / 1e9
     return {"tflops": tf, "mfma_frac": tf / PEAK_BF16_TFLOPS, "gbs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS}
+
+
+def packed_leg(exts, dev, cpu, nthr, torch, args):
+    """GDNLayerCustom.forward(x, cu_seqlens=...) on config 4's 8 packed lengths
+    (U[512, 8192], seed 3) at config 5's dims: RMSNorm, one packed in-projection
+    launch (+ conv + SiLU, per-sequence conv caches), the packed prefill and the
+    W_o GEMM.  MFMA roofline on the layer's algorithmic FLOPs (projections and
+    the prefill's per token-head count); parity: sequence 0 against the oracle
+    layer run on it alone (fp32 projection)."""
+    from gdn_18646_amd import synth
+    from gdn_18646_amd.gdn_layer import GDNLayerCustom, make_weights
+    LD, LH = 2048, 16
+    lengths = synth.varlen_lengths(8, 512, 8192, seed=3)
+    Tt = sum(lengths)
+    gp = torch.Generator().manual_seed(7)
+    w_cpu = make_weights(device="cpu", D=LD, H=LH, DK=128, DV=128, std=0.02, generator=gp)
+    layer = GDNLayerCustom({k: v.to(dev) for k, v in w_cpu.items()}, exts)
+    x_cpu = torch.randn(1, Tt, LD, generator=gp).bfloat16()
+    x = x_cpu.to(dev)
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    y = layer.forward(x, cu_seqlens=cu)
+    ms = time_events(lambda: layer.forward(x, cu_seqlens=cu), max(3, args.steps // 4), torch)
+    ncols = 2 * LH * 128 + LH * 128 + 2 * LH
+    flop = 2 * Tt * LD * ncols + PREFILL_FLOP_PER_TOKEN_HEAD * Tt * LH + 2 * Tt * LH * 128 * LD
+    nbytes = 2 * Tt * LD * 2 + 2 * ncols * LD + 2 * LD * LH * 128 + prefill_bytes(Tt, LH, len(lengths)) - 4 * Tt
+    leg = {"config": f"config 4's lengths {lengths} packed ({Tt} tokens), config 5's layer dims (hidden 2048, H=16, "
+                     "dk=dv=128, conv 4, weights N(0, 0.02)), zero initial state",
+           "ms": ms, "tokens_per_s": Tt / (ms / 1e3), **roofline_fracs(flop, nbytes, ms), "flop": flop, "bytes": nbytes}
+    log(f"layer packed forward ({Tt} tokens, 8 sequences): {ms:.3f} ms, {Tt / (ms / 1e3):.4g} tok/s, "
+        f"{leg['mfma_frac'] * 100:.1f}% of MFMA peak")
+    from oracle.layer_ref import GDNLayerBaseline
+    y0 = y[:, :lengths[0]].cpu()
+    y_ref = GDNLayerBaseline(w_cpu, chunk_size=C, fp32_proj=True).forward(x_cpu[:, :lengths[0]])
+    leg["parity_seq0_vs_oracle_fp32_proj"] = {**out_parity(y0, y_ref), "rel_fro": rel_fro(y0, y_ref)}
+    log(f"  packed layer parity {leg['parity_seq0_vs_oracle_fp32_proj']}")
+    return leg
 
 
 def serve_leg(exts, dev, cpu, nthr, torch):
@@ -577,6 +617,10 @@ def main():
         result["layer_e2e"] = leg
         log(f"  layer parity {leg['parity']}")
         del layer, wl, xl, st_l
+
+    # ------------------------------- packed layer forward (config-4 lengths, config-5 dims)
+    if "packed" in legs:
+        result["layer_packed"] = packed_leg(exts, dev, cpu, nthr, torch, args)
 
     # ------------------------------- layer decode at serving batch sizes (config-5 dims)
     if "serve" in legs:

@@ -24,6 +24,8 @@
 // + SiLU (as the prefill in-projection does), updates the conv caches and
 // the x_n history in place, and writes q/k/v/a/b in the decode kernel's
 // layouts; the out-projection rounds o to bf16 as it loads it.
+#include <algorithm>
+
 #include "gdn_common.hpp"
 #include "proj.hpp"
 
@@ -426,18 +428,41 @@ extern "C" int gdn_in_proj_varlen_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_
         return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: conv caches in and out must not alias");
     const int Hk = H * dk, Hv = H * dv, nc = conv_k - 1;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    for (int i = 0; i < num_seqs; ++i) {
+    auto cin = [&](const gdn_bf16_t* c, int i, int width) {
+        return c ? c + static_cast<size_t>(i) * width * nc : nullptr;
+    };
+    auto cout = [&](gdn_bf16_t* c, int i, int width) { return c ? c + static_cast<size_t>(i) * width * nc : nullptr; };
+    // Parameters for sequences [i, i + 1) ... starting at packed token t0.
+    auto params = [&](int i, int t0) {
+        gdn_proj::ProjParams p = {};
+        p.x = xn + static_cast<size_t>(t0) * D;
+        p.W = W_qkvab;
+        p.conv_w = conv_w_qkv;
+        p.T_out = T_total;
+        p.D = D;
+        p.D_out = 2 * Hk + Hv + 2 * H;
+        p.conv_k = conv_k;
+        p.ngroups = 5;
+        p.groups[0] = gdn_proj::ProjGroup{0, Hk, dk, 1, 0, q + static_cast<size_t>(t0) * dk, cin(cache_q_in, i, Hk),
+                                          cout(cache_q_out, i, Hk)};
+        p.groups[1] = gdn_proj::ProjGroup{Hk, Hk, dk, 1, Hk, k + static_cast<size_t>(t0) * dk, cin(cache_k_in, i, Hk),
+                                          cout(cache_k_out, i, Hk)};
+        p.groups[2] = gdn_proj::ProjGroup{2 * Hk, Hv, dv, 1, 2 * Hk, v + static_cast<size_t>(t0) * dv,
+                                          cin(cache_v_in, i, Hv), cout(cache_v_out, i, Hv)};
+        p.groups[3] = gdn_proj::ProjGroup{2 * Hk + Hv, H, 1, 0, 0, a + t0, nullptr, nullptr};
+        p.groups[4] = gdn_proj::ProjGroup{2 * Hk + Hv + H, H, 1, 0, 0, b + t0, nullptr, nullptr};
+        return p;
+    };
+    // Sequence i on its own (a launch of its tokens, or the cache hand-over of
+    // an empty sequence).
+    auto one_seq = [&](int i) -> int {
         const int t0 = cu_seqlens[i], len = cu_seqlens[i + 1] - t0;
-        auto cin = [&](const gdn_bf16_t* c, int width) {
-            return c ? c + static_cast<size_t>(i) * width * nc : nullptr;
-        };
-        auto cout = [&](gdn_bf16_t* c, int width) { return c ? c + static_cast<size_t>(i) * width * nc : nullptr; };
         if (len == 0) {
             // An empty sequence keeps its conv history (zeros without one).
             const struct { const gdn_bf16_t* in; gdn_bf16_t* out; int width; } caches[3] = {
-                {cin(cache_q_in, Hk), cout(cache_q_out, Hk), Hk},
-                {cin(cache_k_in, Hk), cout(cache_k_out, Hk), Hk},
-                {cin(cache_v_in, Hv), cout(cache_v_out, Hv), Hv}};
+                {cin(cache_q_in, i, Hk), cout(cache_q_out, i, Hk), Hk},
+                {cin(cache_k_in, i, Hk), cout(cache_k_out, i, Hk), Hk},
+                {cin(cache_v_in, i, Hv), cout(cache_v_out, i, Hv), Hv}};
             for (const auto& c : caches) {
                 if (!c.out || nc == 0) continue;
                 const size_t bytes = static_cast<size_t>(c.width) * nc * 2;
@@ -451,31 +476,38 @@ extern "C" int gdn_in_proj_varlen_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_
                     if (rc != GDN_OK) return rc;
                 }
             }
-            continue;
+            return GDN_OK;
         }
-        gdn_proj::ProjParams p = {};
-        p.x = xn + static_cast<size_t>(t0) * D;
+        gdn_proj::ProjParams p = params(i, t0);
         if (!aligned(p.x, 16) || !aligned(W_qkvab, 16))
             return fail(GDN_ERR_INVALID_ARGUMENT, "in_proj_varlen: xn/W need 16-byte alignment");
-        p.W = W_qkvab;
-        p.conv_w = conv_w_qkv;
         p.B = 1;
         p.T = len;
-        p.T_out = T_total;
-        p.D = D;
-        p.D_out = 2 * Hk + Hv + 2 * H;
-        p.conv_k = conv_k;
-        p.ngroups = 5;
-        p.groups[0] = gdn_proj::ProjGroup{0, Hk, dk, 1, 0, q + static_cast<size_t>(t0) * dk, cin(cache_q_in, Hk),
-                                          cout(cache_q_out, Hk)};
-        p.groups[1] = gdn_proj::ProjGroup{Hk, Hk, dk, 1, Hk, k + static_cast<size_t>(t0) * dk, cin(cache_k_in, Hk),
-                                          cout(cache_k_out, Hk)};
-        p.groups[2] = gdn_proj::ProjGroup{2 * Hk, Hv, dv, 1, 2 * Hk, v + static_cast<size_t>(t0) * dv,
-                                          cin(cache_v_in, Hv), cout(cache_v_out, Hv)};
-        p.groups[3] = gdn_proj::ProjGroup{2 * Hk + Hv, H, 1, 0, 0, a + t0, nullptr, nullptr};
-        p.groups[4] = gdn_proj::ProjGroup{2 * Hk + Hv + H, H, 1, 0, 0, b + t0, nullptr, nullptr};
-        const int rc = gdn_proj::launch_proj(p, st);
-        if (rc != GDN_OK) return rc;
+        return gdn_proj::launch_proj(p, st);
+    };
+    // One launch of the MFMA kernel per run of up to kPackMax sequences: its
+    // row space holds every sequence's 3 cache rows and tokens back to back,
+    // so short sequences share tiles and no launch waits for another.  A run
+    // with no tokens (only empty sequences), or a shape the MFMA kernel does
+    // not take, goes sequence by sequence.
+    for (int i = 0; i < num_seqs;) {
+        const int j = std::min(num_seqs, i + gdn_proj::kPackMax);
+        const int t0 = cu_seqlens[i], t1 = cu_seqlens[j];
+        gdn_proj::ProjParams p = params(i, t0);
+        p.B = 1;
+        p.T = t1 - t0;
+        p.packed = j - i;
+        for (int s = 0; s <= j - i; ++s) p.row_off[s] = cu_seqlens[i + s] - t0 + gdn_proj::kCacheRows * s;
+        if (t1 > t0 && aligned(p.x, 16) && gdn_proj::mfma_path_ok(p)) {
+            const int rc = gdn_proj::launch_proj(p, st);
+            if (rc != GDN_OK) return rc;
+        } else {
+            for (int s = i; s < j; ++s) {
+                const int rc = one_seq(s);
+                if (rc != GDN_OK) return rc;
+            }
+        }
+        i = j;
     }
     return GDN_OK;
 }

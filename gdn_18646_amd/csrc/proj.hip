@@ -29,6 +29,7 @@
 // Output routing: up to 5 column groups, each written either token-major
 // [B, T, width] or head-major [B, width/hd, T, hd], with or without the
 // conv + SiLU (a plain projection takes the current token's row of P).
+#include <cstddef>
 #include <type_traits>
 
 #include "gdn_common.hpp"
@@ -221,6 +222,17 @@ __device__ __forceinline__ float tap_prev(float cur, float prev) {
     return __int_as_float(__builtin_amdgcn_update_dpp(rot, __float_as_int(cur), 0x110 + K, 0xf, 0xf, false));
 }
 
+// Packed row table of the launch (ProjParams::row_off), read from the
+// kernel's argument block (the ProjParams argument sits at its start):
+// indexing the by-value parameter with a runtime index would copy it to
+// private memory.
+using kconst_i32 = __attribute__((address_space(4))) const int32_t;
+__device__ __forceinline__ const kconst_i32* packed_rows() {
+    const __attribute__((address_space(4))) char* base =
+        (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
+    return reinterpret_cast<const kconst_i32*>(base + offsetof(gdn_proj::ProjParams, row_off));
+}
+
 // Groups whose output goes out through the LDS output tile in 16-byte
 // chunks: 8-column aligned, 8-column head_dim (or token-major), 16-byte
 // aligned destination.
@@ -259,12 +271,43 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
     }
     const int tile_t = lin / n_col, tile_c = lin % n_col;
     // Row space: each sequence is kHalo cache rows (t = -3 .. -1) followed by
-    // its T tokens, so row r is (b, t) = (r / T3, r % T3 - 3).  Cache rows
-    // take the cached projections (or zero) after the product, so conv taps
-    // never reach into another sequence.
+    // its tokens, so row r is (b, t) = (r / T3, r % T3 - 3) for equal lengths
+    // T, or, for packed sequences, b the last with row_off[b] <= r and
+    // t = r - row_off[b] - 3.  Cache rows take the cached projections (or
+    // zero) after the product, so conv taps never reach into another
+    // sequence.
     const int T3 = p.T + kHalo;
-    const int F3 = p.B * T3;
+    const bool packed = p.packed > 0;  // uniform
+    const kconst_i32* prow = packed_rows();
+    const int nseq = packed ? p.packed : p.B;
+    const int F3 = packed ? prow[p.packed] : p.B * T3;
     const int f0 = tile_t * kMOut - kHalo;  // row of tile row 0 (>= -3; rows < 0 are never used)
+    // Packed: the sequence of the tile's first row (uniform), the start of
+    // every per-row search below.
+    int pb0 = 0;
+    if (packed) {
+        int lo = 0, hi = p.packed;  // prow[lo] <= max(f0, 0) < prow[hi]
+        const int r = max(f0, 0);
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (prow[mid] <= r) lo = mid; else hi = mid;
+        }
+        pb0 = lo;
+    }
+    auto len3 = [&](int b) { return packed ? prow[b + 1] - prow[b] : T3; };     // rows of sequence b
+    auto tok0 = [&](int b) { return packed ? prow[b] - kHalo * b : b * p.T; };  // x row of its first token
+    // (b, t3 = t + 3) of row r >= 0 (packed rows past the last sequence stay in it).
+    auto locate = [&](int r, int& b, int& t3) {
+        if (packed) {
+            int bb = pb0;
+            while (bb + 1 < p.packed && prow[bb + 1] <= r) ++bb;
+            b = bb;
+            t3 = r - prow[bb];
+        } else {
+            b = r / T3;
+            t3 = r - b * T3;
+        }
+    };
     const int c0 = tile_c * kMCols;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: DMA bases stay scalar
@@ -273,11 +316,13 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
 
     // x row feeding row r: the token itself, the sequence's first token for
     // cache rows, clamped at both ends (those products are never used).
+    const int ntok = packed ? F3 - kHalo * p.packed : p.B * p.T;  // x rows
     auto xrow_of = [&](int r) {
         if (r < 0) return 0;
-        if (r >= F3) return p.B * p.T - 1;
-        const int b = r / T3, t = r - b * T3 - kHalo;
-        return b * p.T + max(t, 0);
+        if (r >= F3) return ntok - 1;
+        int b, t3;
+        locate(r, b, t3);
+        return min(tok0(b) + max(t3 - kHalo, 0), ntok - 1);  // an empty last sequence has no token of its own
     };
 
     // DMA sources.  Copy j of a wave moves staged rows 8 q .. 8 q + 7 with
@@ -392,8 +437,12 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
     // nt adds 16 rows.  Rows before local row kHalo are the tile's halo.
     const int nloc0 = 16 * kWNT * wn + r16;
     auto split = [&](int r, int& b, int& t3) {
-        b = r < 0 ? 0 : r / T3;
-        t3 = r - b * T3;
+        if (r < 0) {
+            b = 0;
+            t3 = r;
+        } else {
+            locate(r, b, t3);
+        }
     };
     int b0, t30;
     split(f0 + nloc0, b0, t30);
@@ -408,7 +457,7 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         const int R0 = f0 + 16 * kWNT * wn;
         int bR, t3R;
         split(R0, bR, t3R);
-        lean = R0 >= 0 && R0 + 16 * kWNT <= F3 && t3R >= kHalo && t3R + 16 * kWNT <= T3 - ncache;
+        lean = R0 >= 0 && R0 + 16 * kWNT <= F3 && t3R >= kHalo && t3R + 16 * kWNT <= len3(bR) - ncache;
     }
 
     // Output tile in LDS (the two stages): row = token of the tile (512
@@ -455,7 +504,8 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             const int q = t3 - kHalo + ncache;
             if (conv && t3 < kHalo) {
                 const uint16_t* cin = gq.cache_in;
-                const bool has = cin != nullptr && q >= 0;
+                // (rows past the last sequence, in the last tile, read nothing)
+                const bool has = cin != nullptr && q >= 0 && b < nseq;
                 const uint16_t* src = has ? cin + (static_cast<size_t>(b) * width + cc) * ncache + q : nullptr;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = has ? bf2f(src[i * ncache]) : 0.f;
@@ -471,6 +521,12 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         // hd) T hd + (cc + i) % hd).
         const size_t seq = static_cast<size_t>(width) * p.T_out;
         const int tstride = hd ? hd : width;
+        // token t of sequence b: b width T_out + t tstride, or, packed, its
+        // token offset in the packed outputs times tstride
+        auto orow = [&](int b, int t) {
+            return packed ? static_cast<size_t>(tok0(b) + t) * tstride
+                          : static_cast<size_t>(b) * seq + static_cast<size_t>(t) * tstride;
+        };
         const bool vec = hd == 0 || (hd & 3) == 0;  // the 4 columns are adjacent in memory
         size_t coff[4] = {0, 0, 0, 0};
         if (!staged) {
@@ -498,7 +554,12 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             constexpr int nt = decltype(NT)::value;
             if (nt > 0 && !lean) {
                 t3 += 16;
-                if (t3 >= T3) {
+                if (packed) {
+                    while (b + 1 < p.packed && t3 >= len3(b)) {
+                        t3 -= len3(b);
+                        ++b;
+                    }
+                } else if (t3 >= T3) {
                     b += t3 / T3;
                     t3 %= T3;
                 }
@@ -525,17 +586,18 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
                     u32x2{pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3])};
             } else if (lean) {
                 if (!(nt == 0 && nloc0 < kHalo))  // the tile's halo rows
-                    store(gq.dst + static_cast<size_t>(b0) * seq + static_cast<size_t>(t30 - kHalo + 16 * nt) * tstride, y);
+                    store(gq.dst + orow(b0, t30 - kHalo + 16 * nt), y);
             } else if (nloc >= kHalo && f0 + nloc < F3 && t3 >= kHalo) {
-                store(gq.dst + static_cast<size_t>(b) * seq + static_cast<size_t>(t3 - kHalo) * tstride, y);
+                store(gq.dst + orow(b, t3 - kHalo), y);
             }
             // New cache: rows t = T - ncache .. T - 1 of the extended sequence
             // (cache rows included when T < ncache).
-            if (!lean && conv && gq.cache_out && nloc >= kHalo && f0 + nloc < F3 && t3 - kHalo >= p.T - ncache) {
+            const int Tb = len3(b) - kHalo;
+            if (!lean && conv && gq.cache_out && nloc >= kHalo && f0 + nloc < F3 && t3 - kHalo >= Tb - ncache) {
                 const int t = t3 - kHalo;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    gq.cache_out[(static_cast<size_t>(b) * width + cc + i) * ncache + (t - (p.T - ncache))] =
+                    gq.cache_out[(static_cast<size_t>(b) * width + cc + i) * ncache + (t - (Tb - ncache))] =
                         f2bf_bits(cur[i]);
             }
         });
@@ -564,14 +626,16 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             const int row = row0 + 16 * i;
             if (i > 0) {
                 t3 += 16;
-                while (t3 >= T3) {
-                    t3 -= T3;
+                while ((!packed || b + 1 < p.packed) && t3 >= len3(b)) {
+                    t3 -= len3(b);
                     ++b;
                 }
             }
             if (row >= kHalo && f0 + row < F3 && t3 >= kHalo) {
                 const u32x4 v = *reinterpret_cast<const lds_u32x4*>(otile + ounit(row, j >> 1) + 16 * (j & 1));
-                *reinterpret_cast<u32x4*>(colp + static_cast<size_t>(b) * seq + static_cast<size_t>(t3 - kHalo) * tstride) = v;
+                const size_t o = packed ? static_cast<size_t>(tok0(b) + t3 - kHalo) * tstride
+                                        : static_cast<size_t>(b) * seq + static_cast<size_t>(t3 - kHalo) * tstride;
+                *reinterpret_cast<u32x4*>(colp + o) = v;
             }
         }
     }
@@ -585,12 +649,15 @@ namespace gdn_proj {
 // 4 columns share a group), 8-byte aligned outputs for its vector stores,
 // 16-byte aligned conv weights (read 4 columns x 4 taps at a time) and 32-bit
 // DMA offsets.
-static bool mfma_path_ok(const ProjParams& p) {
+static_assert(kCacheRows == kHalo, "row space");
+
+bool mfma_path_ok(const ProjParams& p) {
     if (p.D % kMK != 0 || p.D_out % 4 != 0) return false;
     if (!gdn_host::aligned(p.conv_w, 16)) return false;
     if (static_cast<long long>(p.D_out) * p.D * 2 >= (1ll << 31)) return false;
     if (static_cast<long long>(kMToks) * p.D * 2 >= (1ll << 31)) return false;
     if (static_cast<long long>(p.B) * (p.T + kHalo) >= (1ll << 30)) return false;
+    if (p.packed < 0 || p.packed > kPackMax) return false;
     for (int g = 0; g < p.ngroups; ++g) {
         const ProjGroup& q = p.groups[g];
         if (q.col0 % 4 != 0 || q.width % 4 != 0 || q.cw_row0 % 4 != 0) return false;
@@ -605,6 +672,15 @@ static bool mfma_path_ok(const ProjParams& p) {
 int launch_proj(const ProjParams& pin, hipStream_t stream) {
     ProjParams p = pin;
     if (p.T_out < p.T) p.T_out = p.T;
+    if (p.packed > 0) {
+        // Packed sequences: the MFMA kernel only (callers check mfma_path_ok
+        // first); rows: kHalo cache rows + the tokens of every sequence.
+        if (!mfma_path_ok(p)) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "proj: packed launch off the MFMA path");
+        const int F3 = p.row_off[p.packed];
+        const int n_tok = (F3 + kMOut - 1) / kMOut, n_col = (p.D_out + kMCols - 1) / kMCols;
+        hipLaunchKernelGGL(gdn_proj_conv_mfma_kernel, dim3(n_tok * n_col), dim3(kMWaves * 64), 0, stream, p, n_tok, n_col);
+        return gdn_host::check_launch("gdn_proj_conv_mfma_kernel");
+    }
     if (p.B == 0 || p.T == 0 || p.D_out == 0) return GDN_OK;
     if (mfma_path_ok(p)) {
         const int F3 = p.B * (p.T + kHalo);  // rows: kHalo cache rows + T tokens per sequence

@@ -8,6 +8,7 @@
 namespace gdn_proj {
 
 constexpr int kMaxGroups = 5;
+constexpr int kPackMax = 256;  // packed sequences per launch of the MFMA kernel
 
 // Columns [col0, col0 + width) of P = x W^T go to dst.  head_dim > 0 writes
 // [B, width / head_dim, T, head_dim]; head_dim == 0 writes [B, T, width].
@@ -36,8 +37,20 @@ struct ProjParams {
     int T_out;    // token stride of the outputs (>= T; 0 = T): a sequence written into a longer packed buffer
     int ngroups;  // groups sorted by col0, groups[0].col0 == 0
     ProjGroup groups[kMaxGroups];
+    // Packed sequences (MFMA kernel only): packed > 0 sequences of unequal
+    // lengths, x [T_total, D] and outputs [.., T_out, ..] token-packed, caches
+    // [packed, width, conv_k - 1].  Sequence i owns rows row_off[i] ..
+    // row_off[i + 1] - 1 of the kernel's row space (3 cache rows, then its
+    // tokens), so row_off[i] = (token offset of sequence i) + 3 i.  The kernel
+    // reads the table from its argument block.
+    int packed;
+    int32_t row_off[kPackMax + 1];
 };
 
+constexpr int kCacheRows = 3;  // rows of the MFMA kernel's row space ahead of each sequence's tokens
+
+// Whether the MFMA kernel takes these parameters (group alignment, sizes).
+bool mfma_path_ok(const ProjParams& p);
 int launch_proj(const ProjParams& p, hipStream_t stream);
 
 }  // namespace gdn_proj

@@ -191,3 +191,49 @@ def test_decode_out_proj_matches_composition(dev, B, K, N):
     with pytest.raises(RuntimeError, match="B=17"):
         lay.decode_out_proj(torch.zeros(17, K, device=dev), W.to(dev))
 
+
+
+# Packed in-projection (gdn_in_proj_varlen_hip): one launch of the MFMA kernel
+# per run of up to 256 sequences, whose row space holds every sequence's 3
+# cache rows and tokens back to back.  Each output row is the same dot product
+# as in a launch of that sequence alone, so the result must equal, bit for bit,
+# the batch entry point run on every sequence by itself (its own cache in, its
+# cache out).  Cases: config 4's lengths at config 5's dims; empty and 1..3
+# token sequences (shorter than the conv window, so the new cache takes cache
+# rows); conv width 2 without caches in; 300 sequences (two launches).
+@pytest.mark.parametrize("lengths,H,dk,dv,D,ck,with_cache", [
+    ([3670, 1053, 3636, 3547, 4688, 709, 2874, 4497], 16, 128, 128, 2048, 4, True),
+    ([0, 1, 2, 5, 0, 300, 64, 3, 0], 4, 32, 16, 128, 4, True),
+    ([1, 2, 3, 250, 0, 17], 4, 32, 16, 128, 2, False),
+    ([7] * 150 + [0, 1] * 75, 4, 32, 16, 128, 4, True),
+])
+def test_in_proj_packed_one_launch_matches_per_sequence(dev, lengths, H, dk, dv, D, ck, with_cache):
+    from gdn_18646_amd import native_extension
+    lay = native_extension().layer
+    N = len(lengths)
+    print(f"packed in_proj case N={N} T_total={sum(lengths)} H={H} D={D} conv {ck}", flush=True)
+    g = torch.Generator().manual_seed(N * 7 + D + ck)
+    Dout = 2 * H * dk + H * dv + 2 * H
+    Tt = sum(lengths)
+    cu = torch.tensor([0] + lengths).cumsum(0).to(torch.int32)
+    x = torch.randn(Tt, D, generator=g).bfloat16().to(dev)
+    W = (torch.randn(Dout, D, generator=g) * D ** -0.5).bfloat16().to(dev)
+    cw = (torch.randn(Dout - 2 * H, ck, generator=g) * 0.5).bfloat16().to(dev)
+    caches = [None] * 3
+    if with_cache:
+        caches = [torch.randn(N, H * d, ck - 1, generator=g).bfloat16().to(dev) for d in (dk, dk, dv)]
+    got = lay.in_proj_varlen(x, W, cw, H, dk, dv, cu, *caches, True)
+    torch.cuda.synchronize()
+    for i in range(N):
+        t0, t1 = int(cu[i]), int(cu[i + 1])
+        cin = [c[i:i + 1] if c is not None else None for c in caches]
+        if t1 == t0:  # an empty sequence keeps its cache (zeros without one)
+            for name, y, c in zip(("cache_q", "cache_k", "cache_v"), got[5:], cin):
+                want = c[0] if c is not None else torch.zeros_like(y[i])
+                assert torch.equal(y[i], want), f"sequence {i} (empty): {name}"
+            continue
+        ref = lay.in_proj(x[t0:t1].unsqueeze(0), W, cw, H, dk, dv, *cin, True)
+        for name, y, r in zip("qkvab", got[:5], ref[:5]):
+            assert torch.equal(y[:, :, t0:t1], r), f"sequence {i} (length {t1 - t0}): {name}"
+        for name, y, r in zip(("cache_q", "cache_k", "cache_v"), got[5:], ref[5:]):
+            assert torch.equal(y[i], r[0]), f"sequence {i} (length {t1 - t0}): {name}"
