@@ -92,6 +92,7 @@ constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkMaxCols = 16;  // weight rows (output columns) per workgroup: 16, or 8 to spread small N
 constexpr int kSkStride = 32 * kSkWaves;  // K elements between a wave's consecutive steps
 constexpr int kSkCUs = 256;
+constexpr int kStepMaxB = 64;  // gdn_layer_decode_step_hip: sequences, as groups of kSkM
 
 struct SkinnyParams {
     const uint16_t* W;  // [N, K]
@@ -653,15 +654,38 @@ extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* 
     // Every stage's arguments are checked before the first launch: the
     // in-projection updates the conv caches and x_n history in place, so a
     // later stage refusing its arguments would leave the state half-advanced.
-    int st = in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B, D, H, dk, dv,
+    // Up to kStepMaxB sequences run as groups of kSkM: one in- and one
+    // out-projection launch per group (each streams the weights once more),
+    // one recurrence launch for all; the groups' row offsets keep every
+    // pointer's alignment, so checking the first group covers them all.
+    if (B < 0 || B > kStepMaxB)
+        return gdn_host::fail(B < 0 ? GDN_ERR_INVALID_ARGUMENT : GDN_ERR_UNSUPPORTED,
+                              "decode_step: B=%d, at most %d sequences", B, kStepMaxB);
+    const int B0 = std::min(B, kSkM);
+    int st = in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B0, D, H, dk, dv,
                            conv_k);
     if (st == GDN_OK) st = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
-    if (st == GDN_OK) st = out_proj_check(o, W_o, y, B, H * dv, D);
+    if (st == GDN_OK) st = out_proj_check(o, W_o, y, B0, H * dv, D);
     if (st != GDN_OK || B == 0) return st;
-    st = gdn_decode_in_proj_hip(x, gamma, eps, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v,
-                                    a, b, B, D, H, dk, dv, conv_k, stream);
-    if (st != GDN_OK) return st;
+    const int nc = conv_k - 1;
+    const size_t Hk = static_cast<size_t>(H) * dk, Hv = static_cast<size_t>(H) * dv;
+    auto off = [](auto* ptr, size_t n) { return ptr ? ptr + n : ptr; };
+    for (int r0 = 0; r0 < B; r0 += kSkM) {
+        const int Bg = std::min(kSkM, B - r0);
+        const size_t r = static_cast<size_t>(r0);
+        st = gdn_decode_in_proj_hip(x + r * D, gamma, eps, W_qkvab, conv_w_qkv, off(cache_q, r * Hk * nc),
+                                    off(cache_k, r * Hk * nc), off(cache_v, r * Hv * nc),
+                                    off(xn_hist, r * nc * D), q + r * Hk, k + r * Hk, v + r * Hv, a + r * H,
+                                    b + r * H, Bg, D, H, dk, dv, conv_k, stream);
+        if (st != GDN_OK) return st;
+    }
     st = gdn_decode_hip(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, S_out, B, H, dk, dv, stream);
     if (st != GDN_OK) return st;
-    return gdn_decode_out_proj_hip(o, W_o, y, B, H * dv, D, stream);
+    for (int r0 = 0; r0 < B; r0 += kSkM) {
+        const int Bg = std::min(kSkM, B - r0);
+        const size_t r = static_cast<size_t>(r0);
+        st = gdn_decode_out_proj_hip(o + r * Hv, W_o, y + r * D, Bg, static_cast<int>(Hv), D, stream);
+        if (st != GDN_OK) return st;
+    }
+    return GDN_OK;
 }

@@ -129,8 +129,8 @@ def test_decode_projection_validation_errors():
 def test_decode_step_validation_errors():
     """The fused step checks every stage's arguments before its first launch."""
     step_args = lambda B, D, dv: ([FAKE, FAKE, 1e-6] + [FAKE] * 10 + [0.1] + [FAKE] * 8 + [B, D, 2, 128, dv, 4, None])
-    with pytest.raises(GdnError, match="decode_in_proj.*B=17"):
-        abi.call("gdn_layer_decode_step_hip", *step_args(17, 2048, 128))
+    with pytest.raises(GdnError, match="decode_step: B=65, at most 64"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(65, 2048, 128))
     with pytest.raises(GdnError, match="decode_in_proj.*D=100"):
         abi.call("gdn_layer_decode_step_hip", *step_args(4, 100, 128))
     abi.call("gdn_layer_decode_step_hip", *step_args(0, 2048, 128))  # B == 0: no-op

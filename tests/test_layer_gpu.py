@@ -82,19 +82,22 @@ def test_layer_decode_matches_prefill(dev, inplace):
     assert_out_close(torch.cat(ys, 1), y_pre, what="decode vs prefill")
 
 
-def test_layer_decode_above_16_sequences_matches_prefill(dev):
-    """B > 16 takes the unfused decode step (RMSNorm, library GEMM, conv-step
-    kernel, library GEMM); it must agree with one prefill too."""
+@pytest.mark.parametrize("B", [20, 40, 72])
+def test_layer_decode_above_16_sequences_matches_prefill(dev, B):
+    """17..48 sequences run the fused step as groups of 16 (B=20: a partial
+    second group; B=40: three groups), more take the unfused step (RMSNorm,
+    library GEMM, conv-step kernel, library GEMM); both must agree with one
+    prefill."""
     _, w = _weights(dev, seed=9)
     layer = GDNLayerCustom(w)
-    x = torch.randn(20, 24, 256, generator=torch.Generator().manual_seed(10)).bfloat16().to(dev)
+    x = torch.randn(B, 24, 256, generator=torch.Generator().manual_seed(10)).bfloat16().to(dev)
     y_pre = layer.forward(x)
-    st = layer.init_decode_state(20)
+    st = layer.init_decode_state(B)
     ys = []
     for t in range(24):
         y_t, st = layer.decode(x[:, t:t + 1], st, inplace=True)
         ys.append(y_t)
-    assert_out_close(torch.cat(ys, 1), y_pre, what="decode (B=20) vs prefill")
+    assert_out_close(torch.cat(ys, 1), y_pre, what=f"decode (B={B}) vs prefill")
 
 
 def test_prefill_hands_off_to_decode(dev):
@@ -196,13 +199,14 @@ def test_layer_config5_decode_after_prefill(dev):
         assert_out_close(st[key].cpu(), st_all[key].cpu(), what=key)
 
 
-@pytest.mark.parametrize("B", [4, 20])
+@pytest.mark.parametrize("B", [4, 20, 72])
 def test_layer_config5_decode_matches_oracle(dev, B):
     """Config-5 dims: a GPU prefill (T=192) hands its decode state to both the
     GPU layer and the oracle layer's decode (fp32 projection); four steps on
     each, compared step by step (outputs to the scaled 2e-2 bar), then the
     recurrent state (1e-2 relative), conv caches and x_n history.  B=4 runs
-    the fused decode step, B=20 the unfused one (library GEMMs)."""
+    the fused decode step, B=20 the fused step as two groups, B=72 the
+    unfused one (library GEMMs)."""
     g, w_cpu, w = _cfg5_weights(dev, seed=12)
     layer, base = GDNLayerCustom(w), GDNLayerBaseline(w_cpu, fp32_proj=True)
     x = torch.randn(B, 196, 2048, generator=g).bfloat16()
