@@ -455,11 +455,22 @@ gdn_prefill_intra_kernel(PrefillParams p) {
             float acc[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) Tc[q] = acc[q] = 0.f;
+            // A[16w + 4q + sub][16w + j] for q = 0..3 (this lane's rows) of
+            // the columns j = 4g .. 4g + 3, read one group of four steps
+            // ahead: each step's row update then waits on no LDS read (a read
+            // per step, consumed by the next, exposed its latency 16 times).
+            f32x4 colA[2][4];
+            auto load_cols = [&](int grp, int slot) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    colA[slot][t] = *reinterpret_cast<const f32x4*>(&Ad[16 * wave + 4 * grp + t][sub * kAQ + 4 * wave]);
+            };
+            load_cols(0, 0);
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int qj = j >> 2, sj = j & 3;
-                // A[16w + 4q + sub][16w + j] for q = 0..3 (this lane's rows)
-                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ad[16 * wave + j][sub * kAQ + 4 * wave]);
+                if (sj == 0 && qj < 3) load_cols(qj + 1, (qj + 1) & 1);
+                const f32x4 a4 = colA[qj & 1][sj];
                 const float own = (j == col ? 1.f : 0.f) - acc[qj];  // row j, valid in lane sub == sj
                 float tj;
                 if (sj == 0) tj = dpp_f<0x00>(own);       // quad_perm [0,0,0,0]
