@@ -1956,12 +1956,13 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact,
             G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
         if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
         s.G = G < 2 ? 1 : static_cast<int>(G);
-        // One group and at most half the CUs busy: split each head's 128
-        // columns over two workgroups of four 16-column compute waves (the
-        // state columns update independently; the halves of a head share K
-        // and Q through the L2 of their XCD, and each wave's chain of
-        // dependent products per chunk is half as long).
-        s.half = s.G == 1 && base <= 128;
+        // At most half the CUs busy in the output pass (equal lengths, or
+        // one group): split each head's 128 columns over two workgroups of
+        // four 16-column compute waves (the state columns update
+        // independently; the halves of a head share K and Q through the L2
+        // of their XCD).  Packed sequences with planned groups keep whole
+        // heads (their plan targets a full round of 128-column workgroups).
+        s.half = (s.G == 1 || !varlen) && base * s.G <= 128;
         if (s.half) s.nvg_out = dv / 64;
         return s;
     }
