@@ -251,6 +251,10 @@ __device__ __forceinline__ gdn_proj::ProjGroup select_group(const gdn_proj::Proj
     return g;
 }
 
+// PACKED: sequences of unequal lengths (ProjParams::packed > 0), rows mapped
+// through the row table; a separate instantiation, so the equal-length kernel
+// carries none of that code.
+template <bool PACKED>
 __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kMWaves / 4, kMWaves / 4))) void gdn_proj_conv_mfma_kernel(
     gdn_proj::ProjParams p, int n_tok, int n_col) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[kMStages * kMStageB + kMHandB];
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
     // zero) after the product, so conv taps never reach into another
     // sequence.
     const int T3 = p.T + kHalo;
-    const bool packed = p.packed > 0;  // uniform
+    constexpr bool packed = PACKED;
     const kconst_i32* prow = packed_rows();
     const int nseq = packed ? p.packed : p.B;
     const int F3 = packed ? prow[p.packed] : p.B * T3;
@@ -316,13 +320,20 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
 
     // x row feeding row r: the token itself, the sequence's first token for
     // cache rows, clamped at both ends (those products are never used).
-    const int ntok = packed ? F3 - kHalo * p.packed : p.B * p.T;  // x rows
     auto xrow_of = [&](int r) {
-        if (r < 0) return 0;
-        if (r >= F3) return ntok - 1;
-        int b, t3;
-        locate(r, b, t3);
-        return min(tok0(b) + max(t3 - kHalo, 0), ntok - 1);  // an empty last sequence has no token of its own
+        if constexpr (PACKED) {
+            const int ntok = F3 - kHalo * p.packed;  // x rows
+            if (r < 0) return 0;
+            if (r >= F3) return ntok - 1;
+            int b, t3;
+            locate(r, b, t3);
+            return min(tok0(b) + max(t3 - kHalo, 0), ntok - 1);  // an empty last sequence has no token of its own
+        } else {
+            if (r < 0) return 0;
+            if (r >= F3) return p.B * p.T - 1;
+            const int b = r / T3, t = r - b * T3 - kHalo;
+            return b * p.T + max(t, 0);
+        }
     };
 
     // DMA sources.  Copy j of a wave moves staged rows 8 q .. 8 q + 7 with
@@ -504,9 +515,11 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             const int q = t3 - kHalo + ncache;
             if (conv && t3 < kHalo) {
                 const uint16_t* cin = gq.cache_in;
-                // (rows past the last sequence, in the last tile, read nothing)
-                const bool has = cin != nullptr && q >= 0 && b < nseq;
-                const uint16_t* src = has ? cin + (static_cast<size_t>(b) * width + cc) * ncache + q : nullptr;
+                const bool has = cin != nullptr && q >= 0;
+                // rows past the last sequence (in the last tile; never stored)
+                // read the last sequence's entries, not past the buffer
+                const uint16_t* src =
+                    has ? cin + (static_cast<size_t>(min(b, nseq - 1)) * width + cc) * ncache + q : nullptr;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = has ? bf2f(src[i * ncache]) : 0.f;
             }
@@ -678,14 +691,16 @@ int launch_proj(const ProjParams& pin, hipStream_t stream) {
         if (!mfma_path_ok(p)) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "proj: packed launch off the MFMA path");
         const int F3 = p.row_off[p.packed];
         const int n_tok = (F3 + kMOut - 1) / kMOut, n_col = (p.D_out + kMCols - 1) / kMCols;
-        hipLaunchKernelGGL(gdn_proj_conv_mfma_kernel, dim3(n_tok * n_col), dim3(kMWaves * 64), 0, stream, p, n_tok, n_col);
+        hipLaunchKernelGGL(gdn_proj_conv_mfma_kernel<true>, dim3(n_tok * n_col), dim3(kMWaves * 64), 0, stream, p, n_tok,
+                           n_col);
         return gdn_host::check_launch("gdn_proj_conv_mfma_kernel");
     }
     if (p.B == 0 || p.T == 0 || p.D_out == 0) return GDN_OK;
     if (mfma_path_ok(p)) {
         const int F3 = p.B * (p.T + kHalo);  // rows: kHalo cache rows + T tokens per sequence
         const int n_tok = (F3 + kMOut - 1) / kMOut, n_col = (p.D_out + kMCols - 1) / kMCols;
-        hipLaunchKernelGGL(gdn_proj_conv_mfma_kernel, dim3(n_tok * n_col), dim3(kMWaves * 64), 0, stream, p, n_tok, n_col);
+        hipLaunchKernelGGL(gdn_proj_conv_mfma_kernel<false>, dim3(n_tok * n_col), dim3(kMWaves * 64), 0, stream, p, n_tok,
+                           n_col);
         return gdn_host::check_launch("gdn_proj_conv_mfma_kernel");
     }
     const dim3 grid((p.T + kOutT - 1) / kOutT, (p.D_out + kBN - 1) / kBN, p.B);
