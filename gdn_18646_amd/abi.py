@@ -42,7 +42,7 @@ SIGNATURES = {
     "gdn_proj_conv_silu_hip": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "gdn_in_proj_hip": (_I, [_P] * 14 + [_I] * 7 + [_P]),
     "gdn_in_proj_varlen_hip": (_I, [_P, _P, _P, _P, _I] + [_P] * 11 + [_I] * 6 + [_P]),
-    "gdn_decode_conv_step_hip": (_I, [_P] * 10 + [_I] * 5 + [_P]),
+    "gdn_decode_conv_step_hip": (_I, [_P] * 12 + [_I] * 6 + [_P]),
     "gdn_decode_in_proj_hip": (_I, [_P, _P, _F] + [_P] * 11 + [_I] * 6 + [_P]),
     "gdn_decode_out_proj_hip": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "gdn_layer_decode_step_hip": (_I, [_P, _P, _F] + [_P] * 10 + [_F] + [_P] * 8 + [_I] * 6 + [_P]),

@@ -335,9 +335,11 @@ std::vector<Tensor> in_proj_varlen(Tensor xn, Tensor W_qkvab, Tensor conv_w_qkv,
     return res;
 }
 
-// Decode conv step on P = xn W^T of one token; caches updated in place.
+// Decode conv step on P = xn W^T of one token; caches updated in place, and,
+// with xn and xn_hist [B, K - 1, D], the x_n history shifted in place.
 std::vector<Tensor> decode_conv_step(Tensor P, Tensor conv_w_qkv, Tensor cache_q, Tensor cache_k, Tensor cache_v,
-                                     int64_t H, int64_t dk, int64_t dv) {
+                                     int64_t H, int64_t dk, int64_t dv, std::optional<Tensor> xn,
+                                     std::optional<Tensor> xn_hist) {
     check_bf16(P, "P");
     check_bf16(conv_w_qkv, "conv_w_qkv");
     const int64_t B = P.size(0);
@@ -350,13 +352,26 @@ std::vector<Tensor> decode_conv_step(Tensor P, Tensor conv_w_qkv, Tensor cache_q
     TORCH_CHECK(cache_q.numel() == B * H * dk * (ck - 1) && cache_k.numel() == B * H * dk * (ck - 1) &&
                     cache_v.numel() == B * H * dv * (ck - 1),
                 "conv caches must be [B, H d, K - 1]");
+    const gdn_bf16_t* xn_ptr = nullptr;
+    gdn_bf16_t* hist = nullptr;
+    int64_t D = 0;
+    if (xn_hist.has_value() && xn_hist->defined() && xn_hist->numel() > 0) {
+        TORCH_CHECK(xn.has_value() && xn->defined(), "xn_hist needs xn");
+        check_bf16(*xn, "xn");
+        check_bf16(*xn_hist, "xn_hist");
+        D = xn->size(-1);
+        TORCH_CHECK(xn->numel() == B * D, "xn must be [B, D]");
+        TORCH_CHECK(xn_hist->numel() == B * (ck - 1) * D, "xn_hist must be [B, K - 1, D]");
+        xn_ptr = bf(*xn);
+        hist = bf_mut(*xn_hist);
+    }
     const c10::DeviceGuard guard(P.device());
     auto o = P.options();
     auto q = at::empty({B, H, dk}, o), k = at::empty({B, H, dk}, o), v = at::empty({B, H, dv}, o);
     auto a = at::empty({B, H}, o), b = at::empty({B, H}, o);
     GDN_CHECK_STATUS(gdn_decode_conv_step_hip(bf(P), bf(conv_w_qkv), bf_mut(cache_q), bf_mut(cache_k), bf_mut(cache_v),
-                                              bf_mut(q), bf_mut(k), bf_mut(v), bf_mut(a), bf_mut(b), B, H, dk, dv, ck,
-                                              stream_of(P)),
+                                              xn_ptr, hist, bf_mut(q), bf_mut(k), bf_mut(v), bf_mut(a), bf_mut(b), B, D,
+                                              H, dk, dv, ck, stream_of(P)),
                      "decode_conv_step");
     return {q, k, v, a, b};
 }
@@ -504,9 +519,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            py::arg("xn"), py::arg("W_qkvab"), py::arg("conv_w_qkv"), py::arg("H"), py::arg("dk"), py::arg("dv"),
            py::arg("cu_seqlens"), py::arg("cache_q") = py::none(), py::arg("cache_k") = py::none(),
            py::arg("cache_v") = py::none(), py::arg("want_cache") = false);
-    ml.def("decode_conv_step", &decode_conv_step, "Decode conv step with projected-token caches (in place)",
+    ml.def("decode_conv_step", &decode_conv_step,
+           "Decode conv step with projected-token caches (in place); with xn and xn_hist also shifts the x_n history",
            py::arg("P"), py::arg("conv_w_qkv"), py::arg("cache_q"), py::arg("cache_k"), py::arg("cache_v"),
-           py::arg("H"), py::arg("dk"), py::arg("dv"));
+           py::arg("H"), py::arg("dk"), py::arg("dv"), py::arg("xn") = py::none(), py::arg("xn_hist") = py::none());
     ml.def("decode_in_proj", &decode_in_proj,
            "Decode step (B <= 16): RMSNorm + q/k/v/a/b projection + conv step + SiLU; caches and xn_hist in place",
            py::arg("x"), py::arg("gamma"), py::arg("eps"), py::arg("W_qkvab"), py::arg("conv_w_qkv"),

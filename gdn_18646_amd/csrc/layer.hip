@@ -41,22 +41,36 @@ struct ConvStepParams {
     int col0[5];
     int width[5];
     int B, Dp, conv_k;
+    const uint16_t* xn;      // [B, D] (with xn_hist): the new token's x_n
+    uint16_t* xn_hist;       // [B, conv_k - 1, D] (nullable): shifted by one token, x_n appended
+    int D;
 };
 
+// Grid: x over Dp + D columns (D only with a history), y = sequence.  Column
+// c < Dp: conv step + SiLU of P's column c (q/k/v) or the plain value (a/b);
+// column Dp + d: the x_n history of feature d moves one token older and takes
+// x_n[d] as the newest (each thread shifts one feature, so in place is safe).
 __global__ __launch_bounds__(256) void gdn_decode_conv_step_kernel(ConvStepParams p) {
-    const long long idx = blockIdx.x * 256ll + threadIdx.x;
-    if (idx >= static_cast<long long>(p.B) * p.Dp) return;
-    const int b = static_cast<int>(idx / p.Dp);
-    const int c = static_cast<int>(idx % p.Dp);
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int b = blockIdx.y;
+    const int nc = p.conv_k - 1;
+    if (c >= p.Dp) {
+        const int d = c - p.Dp;
+        if (!p.xn_hist || d >= p.D || nc == 0) return;
+        uint16_t* h = p.xn_hist + static_cast<size_t>(b) * nc * p.D + d;
+        for (int j = 0; j + 1 < nc; ++j) h[static_cast<size_t>(j) * p.D] = h[static_cast<size_t>(j + 1) * p.D];
+        h[static_cast<size_t>(nc - 1) * p.D] = p.xn[static_cast<size_t>(b) * p.D + d];
+        return;
+    }
     int gi = 0;
 #pragma unroll
     for (int q = 1; q < 5; ++q)
         if (c >= p.col0[q]) gi = q;
     const int cc = c - p.col0[gi];
+    const size_t idx = static_cast<size_t>(b) * p.Dp + c;
     const float pn = bf2f(p.P[idx]);
     float y;
     if (gi < 3) {
-        const int nc = p.conv_k - 1;
         uint16_t* cache = p.cache[gi] + (static_cast<size_t>(b) * p.width[gi] + cc) * nc;
         const uint16_t* w = p.conv_w + static_cast<size_t>(c) * p.conv_k;
         float s = bf2f(w[nc]) * pn;
@@ -514,16 +528,19 @@ extern "C" int gdn_in_proj_varlen_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_
 }
 
 extern "C" int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* conv_w_qkv, gdn_bf16_t* cache_q,
-                                        gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, gdn_bf16_t* q, gdn_bf16_t* k,
-                                        gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b, int B, int H, int dk, int dv,
-                                        int conv_k, void* stream) {
+                                        gdn_bf16_t* cache_k, gdn_bf16_t* cache_v, const gdn_bf16_t* xn,
+                                        gdn_bf16_t* xn_hist, gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v,
+                                        gdn_bf16_t* a, gdn_bf16_t* b, int B, int D, int H, int dk, int dv, int conv_k,
+                                        void* stream) {
     using gdn_host::fail;
-    if (B < 0 || H <= 0 || dk <= 0 || dv <= 0)
-        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_conv_step: B=%d H=%d dk=%d dv=%d", B, H, dk, dv);
+    if (B < 0 || H <= 0 || dk <= 0 || dv <= 0 || (xn_hist && D <= 0))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_conv_step: B=%d H=%d dk=%d dv=%d D=%d", B, H, dk, dv, D);
     if (conv_k < 1 || conv_k > 4)
         return fail(GDN_ERR_UNSUPPORTED, "decode_conv_step: conv_k=%d must be in 1..4", conv_k);
+    if (B > 65535) return fail(GDN_ERR_UNSUPPORTED, "decode_conv_step: B=%d, at most 65535 sequences", B);
     if (B == 0) return GDN_OK;
-    if (!P || !conv_w_qkv || !q || !k || !v || !a || !b || (conv_k > 1 && (!cache_q || !cache_k || !cache_v)))
+    if (!P || !conv_w_qkv || !q || !k || !v || !a || !b || (conv_k > 1 && (!cache_q || !cache_k || !cache_v)) ||
+        (xn_hist && conv_k > 1 && !xn))
         return fail(GDN_ERR_INVALID_ARGUMENT, "decode_conv_step: null pointer argument");
     ConvStepParams p = {};
     p.P = P;
@@ -546,8 +563,11 @@ extern "C" int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* c
     p.B = B;
     p.Dp = 2 * Hk + Hv + 2 * H;
     p.conv_k = conv_k;
-    const long long n = static_cast<long long>(B) * p.Dp;
-    hipLaunchKernelGGL(gdn_decode_conv_step_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+    p.xn = xn;
+    p.xn_hist = conv_k > 1 ? xn_hist : nullptr;
+    p.D = xn_hist ? D : 0;
+    const int ncols = p.Dp + p.D;
+    hipLaunchKernelGGL(gdn_decode_conv_step_kernel, dim3((ncols + 255) / 256, B), dim3(256), 0,
                        static_cast<hipStream_t>(stream), p);
     return gdn_host::check_launch("gdn_decode_conv_step_kernel");
 }

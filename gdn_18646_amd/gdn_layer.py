@@ -264,14 +264,14 @@ class GDNLayerCustom:
             if inplace:
                 return y, state
             return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist)
-        # Shapes the fused step does not take (B > 16, wide D): library GEMMs
+        # Shapes the fused step does not take (B > 48, wide D): library GEMMs
         # around the conv-step and decode kernels.
         xn = self._rmsnorm(x.reshape(B, Dd))
         P = xn @ self.W_qkvab.T
-        q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv)
-        xn_hist = torch.cat([state['xn'], xn.reshape(B, 1, Dd)], 1)[:, 1:]
-        if inplace:
-            state['xn'].copy_(xn_hist)  # same tensor, so a captured step stays valid
+        # the conv-step launch also shifts the x_n history (in place: the
+        # state's own tensor, so a captured step stays valid, or a copy)
+        xn_hist = state['xn'] if inplace else state['xn'].clone()
+        q, k, v, a, b = self._layer.decode_conv_step(P, self.conv_qkv, cq, ck, cv, Hh, dk, dv, xn, xn_hist)
         o = torch.empty(B, Hh, dv, dtype=torch.float32, device=x.device)
         self.exts['decode'].forward(q, k, v, a, b, self.A_log, self.dt_bias_vec, state['recurrent'], self.scale,
                                     o, S_out)

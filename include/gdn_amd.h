@@ -260,13 +260,17 @@ int gdn_in_proj_varlen_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, cons
  * token (columns q|k|v|a|b).  q/k/v columns go through the causal conv over
  * the cached previous conv_k - 1 projections (cache_* [B, H d, conv_k - 1],
  * updated in place) and SiLU; a/b pass through.  Outputs in the decode
- * kernel's layouts: q, k [B, H, dk]; v [B, H, dv]; a, b [B, H].
+ * kernel's layouts: q, k [B, H, dk]; v [B, H, dv]; a, b [B, H].  With
+ * xn_hist [B, conv_k - 1, D] (nullable) the same launch also moves the x_n
+ * history one token older and appends xn [B, D] (the layer's decode-state
+ * `xn`).  B <= 65535.
  * Replaces _decode_conv_step / _decode_fused_proj_step (gdn_layer.py:43-69).
  */
 int gdn_decode_conv_step_hip(const gdn_bf16_t* P, const gdn_bf16_t* conv_w_qkv,
                              gdn_bf16_t* cache_q, gdn_bf16_t* cache_k, gdn_bf16_t* cache_v,
+                             const gdn_bf16_t* xn, gdn_bf16_t* xn_hist,
                              gdn_bf16_t* q, gdn_bf16_t* k, gdn_bf16_t* v, gdn_bf16_t* a, gdn_bf16_t* b,
-                             int B, int H, int dk, int dv, int conv_k, void* stream);
+                             int B, int D, int H, int dk, int dv, int conv_k, void* stream);
 
 /*
  * One decode step's input side for B <= 16 sequences: x_n = RMSNorm(x)

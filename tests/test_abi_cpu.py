@@ -126,6 +126,17 @@ def test_decode_projection_validation_errors():
         abi.call("gdn_decode_out_proj_hip", FAKE + 4, FAKE, FAKE, 4, 2048, 2048, None)
 
 
+def test_decode_conv_step_validation_errors():
+    args = lambda B, D, ck, hist: ([FAKE] * 5 + [FAKE, FAKE if hist else None] + [FAKE] * 5 + [B, D, 2, 128, 64, ck, None])
+    with pytest.raises(GdnError, match="B=70000, at most 65535"):
+        abi.call("gdn_decode_conv_step_hip", *args(70000, 256, 4, True))
+    with pytest.raises(GdnError, match="D=0"):
+        abi.call("gdn_decode_conv_step_hip", *args(4, 0, 4, True))
+    with pytest.raises(GdnError, match="conv_k=5"):
+        abi.call("gdn_decode_conv_step_hip", *args(4, 256, 5, False))
+    abi.call("gdn_decode_conv_step_hip", *args(0, 256, 4, True))  # B == 0: no-op
+
+
 def test_decode_step_validation_errors():
     """The fused step checks every stage's arguments before its first launch."""
     step_args = lambda B, D, dv: ([FAKE, FAKE, 1e-6] + [FAKE] * 10 + [0.1] + [FAKE] * 8 + [B, D, 2, 128, dv, 4, None])
