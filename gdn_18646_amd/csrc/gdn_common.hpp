@@ -195,4 +195,9 @@ inline bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_
 int decode_check(const void* q, const void* k, const void* v, const void* a, const void* b, const void* A_log,
                  const void* dt_bias, const void* S_in, const void* o, const void* S_out, int B, int H, int dk,
                  int dv);
+// RMSNorm of R rows (defined in rmsnorm.hip; arguments already checked as
+// gdn_rmsnorm_hip checks them).  hist (nc > 0): the rows' x_n history
+// [R, nc, D] (nc <= 3), shifted one token older with y appended, in place.
+int rmsnorm_launch(const void* x, const void* gamma, void* y, void* hist, int nc, int R, int D, float eps,
+                   hipStream_t stream);
 }  // namespace gdn_host

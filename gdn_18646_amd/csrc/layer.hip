@@ -106,7 +106,8 @@ constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkMaxCols = 16;  // weight rows (output columns) per workgroup: 16, or 8 to spread small N
 constexpr int kSkStride = 32 * kSkWaves;  // K elements between a wave's consecutive steps
 constexpr int kSkCUs = 256;
-constexpr int kStepMaxB = 64;  // gdn_layer_decode_step_hip: sequences, as groups of kSkM
+constexpr int kStepSkinnyMaxB = 48;  // gdn_layer_decode_step_hip: up to here groups of kSkM, above it tiles
+constexpr int kStepMaxB = 65535;     // gdn_layer_decode_step_hip: sequences
 
 struct SkinnyParams {
     const uint16_t* W;  // [N, K]
@@ -366,6 +367,343 @@ int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
     return gdn_host::check_launch(who);
 }
 
+// ---------------------------------------------------------------------------
+// Decode-step projections for larger batches: 64 x 64 output tiles
+// (sequences x weight rows) on MFMA.
+//
+// The skinny kernel streams the weights once per group of 16 sequences; here
+// the row tiles of one weight tile are dispatched to the same XCD, so the
+// weights cross HBM about once and the row tiles share them through that
+// XCD's L2.  K moves through LDS in 64-wide slices, DMA'd into a ring of
+// stages.  Eight waves: waves 0-3 take the first 32 K of every slice, waves
+// 4-7 the second, each wave a 32 x 32 block of the tile; the two halves'
+// sums meet in LDS at the end.  (A workgroup's load rate grows with its wave
+// count -- measured from L2, 4 waves pull ~90 GB/s, 8 waves ~130 -- and the
+// K split keeps LDS reads at one pass over each slice.)  In LDS, tile rows
+// sit in 1 KB blocks with their 16-byte chunks XOR-swizzled, so the 16 lanes
+// of an operand read (16 rows, one chunk) hit 16 different bank groups.
+//
+// MODE 0, the in-projection: A = x_n [B, K] bf16, W = [W_q; W_k; W_v; W_a;
+// W_b].  P = x_n W^T stays fp32 for the conv step (as in the skinny kernel):
+// q/k/v take SiLU(conv over the cached tokens and P), their caches shift one
+// token in place, a and b take P.  MODE 1, the out-projection: A = o [B, K]
+// fp32, rounded to bf16 as the MFMA operand is built; y = bf16(o W_o^T).
+// ---------------------------------------------------------------------------
+constexpr int kTlM = 64;    // sequences per tile
+constexpr int kTlN = 64;    // weight rows (output columns) per tile
+constexpr int kTlK = 64;    // K per LDS stage
+constexpr int kTlWaves = 8;
+constexpr int kTlThreads = 64 * kTlWaves;
+constexpr int kTlEC = kTlM * kTlN / kTlThreads;  // epilogue columns per thread (8)
+constexpr int kTlPitch = kTlN + 4;  // fp32 words per row of the epilogue's P tile (16-byte rows, no conflicts)
+
+struct TileParams {
+    const uint16_t* W;       // [N, K]
+    int B, K, N;
+    int mtiles, ntiles;
+    const uint16_t* xn;      // MODE 0: x_n [B, K] bf16
+    const float* o;          // MODE 1: o [B, K] fp32
+    uint16_t* y;             // MODE 1: y [B, N] bf16
+    const uint16_t* conv_w;  // MODE 0: [2 H dk + H dv, conv_k]
+    int conv_k;
+    uint16_t* cache[3];      // q, k, v: [B, width, conv_k - 1] bf16, oldest first, updated in place
+    uint16_t* dst[5];        // q, k [B, H dk]; v [B, H dv]; a, b [B, H]
+    int col0[5];
+    int width[5];
+};
+
+template <int MODE>
+struct TileCfg {
+    static constexpr int kABytes = kTlM * kTlK * (MODE == 0 ? 2 : 4);  // A slice of one stage
+    static constexpr int kBBytes = kTlN * kTlK * 2;
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int kStages = 4;
+    static constexpr int kADma = kABytes / (1024 * kTlWaves);  // 1 KB DMA instructions per wave per stage
+    static constexpr int kBDma = kBBytes / (1024 * kTlWaves);
+    static constexpr int kDma = kADma + kBDma;
+    static constexpr int kRingBytes = kStages * kStageBytes;
+    static constexpr int kTapOff = kRingBytes;  // MODE 0: conv taps [kTlN][4] bf16, right-aligned
+    static constexpr int kLdsBytes = kRingBytes + (MODE == 0 ? kTlN * 8 : 0);
+    static_assert(kTlM * kTlPitch * 4 <= kRingBytes, "the epilogue's P tile reuses the ring");
+    static_assert(kADma >= 1 && kBDma >= 1, "every wave issues whole 1 KB blocks");
+};
+
+// Byte offset in a stage of (row r, 16-byte chunk c) of a bf16 slice (8
+// chunks a row, 8 rows a KB) and of an fp32 slice (16 chunks, 4 rows a KB).
+__device__ __forceinline__ uint32_t tl_off_bf16(int r, int c) {
+    return (r >> 3) * 1024 + (r & 7) * 128 + ((c ^ ((r >> 1) & 7)) << 4);
+}
+__device__ __forceinline__ uint32_t tl_off_f32(int r, int c) {
+    return (r >> 2) * 1024 + (r & 3) * 256 + ((c ^ (r & 15)) << 4);
+}
+
+template <int N>
+struct U16Arr { uint16_t v[N]; };
+template <int N>
+struct U4Arr { u32x4 v[N]; };
+
+// NC = conv_k - 1 (MODE 0; 0 for MODE 1).
+template <int MODE, int NC>
+__global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams p) {
+    using Cfg = TileCfg<MODE>;
+    __shared__ __attribute__((aligned(1024))) unsigned char s_tile[Cfg::kLdsBytes];
+    lds_u8* const ring = (lds_u8*)&s_tile[0];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Tile of this workgroup: workgroup id i runs on XCD i % 8; the row tiles
+    // of column tile nt are ids with the same i % 8, so they share one L2.
+    const int id = blockIdx.x, xcd = id & 7, j8 = id >> 3;
+    const int mt = j8 % p.mtiles, nt = xcd + 8 * (j8 / p.mtiles);
+    if (nt >= p.ntiles) return;
+    const int m0 = mt * kTlM, n0 = nt * kTlN;
+    const int nk = p.K / kTlK;
+    // K slice order: column tile nt starts at slice nt % nk, so the
+    // workgroups are spread over the slices (and the memory channels that
+    // hold them) rather than all on the same one; row tiles of one column
+    // tile keep the same order and share its weight slices through L2.
+    const int kstart = nt % nk;
+
+    // Output group of the tile (uniform): q/k/v tiles never straddle groups
+    // (their widths are multiples of kTlN); a and b share the tiles after v.
+    const int g = MODE == 0 ? (n0 >= p.col0[3] ? 3 : n0 >= p.col0[2] ? 2 : n0 >= p.col0[1] ? 1 : 0) : 0;
+    const bool conv_tile = MODE == 0 && g < 3;
+
+    // Epilogue ownership: thread t takes row t / 8 of the tile, columns
+    // 8 (t % 8) .. + 7.
+    const int er = tid >> 3, ec0 = kTlEC * (tid & 7);
+    const int eb = m0 + er;
+    const int eb_ld = min(eb, p.B - 1);
+
+    // Conv-tile inputs load first and are held through the K loop: the
+    // thread's cached tokens (8 NC bf16, contiguous) and, for threads
+    // t < 64, the conv taps of column n0 + t.
+    u32x4 hold[NC > 0 ? NC : 1];
+    uint16_t tap[4] = {0, 0, 0, 0};
+    int cwidth = 0, ccol = 0;
+    uint16_t* cbase = nullptr;
+    if constexpr (MODE == 0) {
+        if (conv_tile) {
+            cbase = g == 0 ? p.cache[0] : g == 1 ? p.cache[1] : p.cache[2];
+            cwidth = g == 0 ? p.width[0] : g == 1 ? p.width[1] : p.width[2];
+            const int gc0 = g == 0 ? p.col0[0] : g == 1 ? p.col0[1] : p.col0[2];
+            ccol = n0 - gc0 + ec0;
+            if constexpr (NC > 0) {
+                const auto crs = buffer_rsrc(cbase, static_cast<uint32_t>(p.B) * cwidth * NC * 2);
+                const uint32_t voff = static_cast<uint32_t>((eb_ld * cwidth + ccol) * NC) * 2;
+#pragma unroll
+                for (int u = 0; u < NC; ++u) hold[u] = buffer_load16(crs, voff, 16 * u);
+            }
+            if (tid < kTlN) {
+                const uint16_t* wr = p.conv_w + static_cast<size_t>(n0 + tid) * (NC + 1);
+#pragma unroll
+                for (int e = 0; e <= NC; ++e) tap[3 - NC + e] = wr[e];
+            }
+        }
+    }
+
+    // DMA source offsets (bytes from the slice's first K column) of this
+    // lane's chunk in each of its 1 KB blocks.
+    const uint16_t* const Wt = p.W + static_cast<size_t>(n0) * p.K;
+    uint32_t aoff[Cfg::kADma], boff[Cfg::kBDma];
+#pragma unroll
+    for (int u = 0; u < Cfg::kBDma; ++u) {
+        const int r = 8 * (wave + kTlWaves * u) + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        boff[u] = static_cast<uint32_t>(min(r, p.N - 1 - n0) * p.K + 8 * c) * 2;
+    }
+#pragma unroll
+    for (int u = 0; u < Cfg::kADma; ++u) {
+        if constexpr (MODE == 0) {
+            const int r = 8 * (wave + kTlWaves * u) + (lane >> 3);
+            const int c = (lane & 7) ^ ((r >> 1) & 7);
+            aoff[u] = static_cast<uint32_t>(min(m0 + r, p.B - 1) * p.K + 8 * c) * 2;
+        } else {
+            const int r = 4 * (wave + kTlWaves * u) + (lane >> 4);
+            const int c = (lane & 15) ^ (r & 15);
+            aoff[u] = static_cast<uint32_t>(min(m0 + r, p.B - 1) * p.K + 4 * c) * 4;
+        }
+    }
+    auto issue = [&](int ks, int slot) {
+        lds_u8* const st = ring + slot * Cfg::kStageBytes;
+        const int k0 = (ks + kstart < nk ? ks + kstart : ks + kstart - nk) * kTlK;
+#pragma unroll
+        for (int u = 0; u < Cfg::kADma; ++u) {
+            if constexpr (MODE == 0)
+                dma16(p.xn + k0, aoff[u], st + (wave + kTlWaves * u) * 1024);
+            else
+                dma16(p.o + k0, aoff[u], st + (wave + kTlWaves * u) * 1024);
+        }
+#pragma unroll
+        for (int u = 0; u < Cfg::kBDma; ++u) dma16(Wt + k0, boff[u], st + Cfg::kABytes + (wave + kTlWaves * u) * 1024);
+    };
+
+    // wave = 4 kh + 2 wm + wn: K half kh of every slice, rows 32 wm, columns 32 wn
+    const int kh = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int kc = 4 * kh + g4;  // the lane's 16-byte chunk of every slice row
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    constexpr int S = Cfg::kStages;
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (s < nk) issue(s, s);
+    for (int i = 0; i < nk; ++i) {
+        // Slice i has landed when at most the S - 2 slices issued after it
+        // are in flight (fewer are issued near the end: wait for all).
+        if (i + S - 2 < nk)
+            wait_vm<(S - 2) * Cfg::kDma>();
+        else
+            wait_vm<0>();
+        // Every wave's part of slice i is in LDS, and every wave is done
+        // with slice i - 1, whose slot the next issue refills.
+        lds_barrier();
+        if (i + S - 1 < nk) issue(i + S - 1, (i + S - 1) % S);
+        const lds_u8* const sa = ring + (i % S) * Cfg::kStageBytes;
+        const lds_u8* const sb = sa + Cfg::kABytes;
+        bf16x8 af[2], bw[2];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            const int r = 32 * wm + 16 * mi + r16;
+            if constexpr (MODE == 0) {
+                af[mi] = *reinterpret_cast<const lds_bf16x8*>(sa + tl_off_bf16(r, kc));
+            } else {
+                const f32x4 lo = *reinterpret_cast<const lds_f32x4*>(sa + tl_off_f32(r, 2 * kc));
+                const f32x4 hi = *reinterpret_cast<const lds_f32x4*>(sa + tl_off_f32(r, 2 * kc + 1));
+                af[mi] = pack8(lo, hi);
+            }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+            bw[ni] = *reinterpret_cast<const lds_bf16x8*>(sb + tl_off_bf16(32 * wn + 16 * ni + r16, kc));
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma16x16x32(af[mi], bw[ni], acc[mi][ni]);
+    }
+
+    // P tile [kTlM][kTlPitch] fp32 over the ring (every wave is past its
+    // last read of it after the first barrier): the second K half's sums,
+    // then the first half's added.
+    lds_barrier();
+    lds_f32* const ps = (lds_f32*)ring;
+    auto ps_at = [&](int mi, int ni, int e) {
+        return (32 * wm + 16 * mi + 4 * g4 + e) * kTlPitch + 32 * wn + 16 * ni + r16;
+    };
+    if (kh == 1) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ps[ps_at(mi, ni, e)] = acc[mi][ni][e];
+    }
+    if constexpr (MODE == 0) {
+        if (conv_tile && tid < kTlN)
+            *reinterpret_cast<lds_u32x2*>(ring + Cfg::kTapOff + 8 * tid) =
+                u32x2{static_cast<uint32_t>(tap[0]) | (static_cast<uint32_t>(tap[1]) << 16),
+                      static_cast<uint32_t>(tap[2]) | (static_cast<uint32_t>(tap[3]) << 16)};
+    }
+    lds_barrier();
+    if (kh == 0) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ps[ps_at(mi, ni, e)] = acc[mi][ni][e] + ps[ps_at(mi, ni, e)];
+    }
+    lds_barrier();
+    if (eb >= p.B) return;
+    float P[kTlEC];
+#pragma unroll
+    for (int u = 0; u < kTlEC / 4; ++u) {
+        const f32x4 v = *reinterpret_cast<const lds_f32x4*>(ring + 4 * (er * kTlPitch + ec0 + 4 * u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) P[4 * u + e] = v[e];
+    }
+    if constexpr (MODE == 1) {
+        if (n0 + ec0 >= p.N) return;
+        *reinterpret_cast<u32x4*>(p.y + static_cast<size_t>(eb) * p.N + n0 + ec0) =
+            u32x4{pack2_bf16(P[0], P[1]), pack2_bf16(P[2], P[3]), pack2_bf16(P[4], P[5]), pack2_bf16(P[6], P[7])};
+    } else if (!conv_tile) {
+        // a / b columns: per column (the a | b boundary may fall inside the
+        // thread's 8).
+#pragma unroll
+        for (int j = 0; j < kTlEC; ++j) {
+            const int n = n0 + ec0 + j;
+            if (n < p.N) {
+                const int gi = n >= p.col0[4] ? 4 : 3;
+                uint16_t* const d = gi == 4 ? p.dst[4] : p.dst[3];
+                const int w = gi == 4 ? p.width[4] : p.width[3];
+                d[static_cast<size_t>(eb) * w + (n - (gi == 4 ? p.col0[4] : p.col0[3]))] = f2bf_bits(P[j]);
+            }
+        }
+    } else {
+        // Conv taps of the 8 columns (4 bf16 each, right-aligned: slot 3
+        // multiplies the new token, slots 3 - NC .. 2 the cached tokens,
+        // oldest first).
+        U16Arr<4 * kTlEC> tp;
+        {
+            U4Arr<kTlEC / 2> t4;
+#pragma unroll
+            for (int u = 0; u < kTlEC / 2; ++u)
+                t4.v[u] = *reinterpret_cast<const lds_u32x4*>(ring + Cfg::kTapOff + 8 * ec0 + 16 * u);
+            tp = __builtin_bit_cast(U16Arr<4 * kTlEC>, t4);
+        }
+        float yv[kTlEC];
+        U16Arr<(NC > 0 ? kTlEC * NC : 1)> nwc;
+        U16Arr<(NC > 0 ? kTlEC * NC : 1)> old;
+        if constexpr (NC > 0) {
+            U4Arr<NC> h;
+#pragma unroll
+            for (int u = 0; u < NC; ++u) h.v[u] = hold[u];
+            old = __builtin_bit_cast(U16Arr<kTlEC * NC>, h);
+        }
+#pragma unroll
+        for (int j = 0; j < kTlEC; ++j) {
+            float s = bf2f(tp.v[4 * j + 3]) * P[j];
+#pragma unroll
+            for (int e = 0; e < NC; ++e) s += bf2f(tp.v[4 * j + 3 - NC + e]) * bf2f(old.v[NC * j + e]);
+#pragma unroll
+            for (int e = 0; e + 1 < NC; ++e) nwc.v[NC * j + e] = old.v[NC * j + e + 1];
+            if constexpr (NC > 0) nwc.v[NC * j + NC - 1] = f2bf_bits(P[j]);
+            yv[j] = silu_f(s);
+        }
+        uint16_t* const d = g == 0 ? p.dst[0] : g == 1 ? p.dst[1] : p.dst[2];
+        *reinterpret_cast<u32x4*>(d + static_cast<size_t>(eb) * cwidth + ccol) =
+            u32x4{pack2_bf16(yv[0], yv[1]), pack2_bf16(yv[2], yv[3]), pack2_bf16(yv[4], yv[5]),
+                  pack2_bf16(yv[6], yv[7])};
+        if constexpr (NC > 0) {
+            const U4Arr<NC> nw = __builtin_bit_cast(U4Arr<NC>, nwc);
+            u32x4* cq = reinterpret_cast<u32x4*>(cbase + (static_cast<size_t>(eb) * cwidth + ccol) * NC);
+#pragma unroll
+            for (int u = 0; u < NC; ++u) cq[u] = nw.v[u];
+        }
+    }
+}
+
+template <int MODE>
+int launch_tile(TileParams& p, hipStream_t st, const char* who) {
+    p.mtiles = (p.B + kTlM - 1) / kTlM;
+    p.ntiles = (p.N + kTlN - 1) / kTlN;
+    const dim3 grid(p.mtiles * ((p.ntiles + 7) / 8) * 8);
+    if constexpr (MODE == 1) {
+        hipLaunchKernelGGL((gdn_decode_tile_kernel<1, 0>), grid, dim3(kTlThreads), 0, st, p);
+    } else {
+        switch (p.conv_k - 1) {
+            case 0: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 0>), grid, dim3(kTlThreads), 0, st, p); break;
+            case 1: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 1>), grid, dim3(kTlThreads), 0, st, p); break;
+            case 2: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 2>), grid, dim3(kTlThreads), 0, st, p); break;
+            default: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 3>), grid, dim3(kTlThreads), 0, st, p); break;
+        }
+    }
+    return gdn_host::check_launch(who);
+}
+
 }  // namespace
 
 extern "C" int gdn_in_proj_hip(const gdn_bf16_t* xn, const gdn_bf16_t* W_qkvab, const gdn_bf16_t* conv_w_qkv,
@@ -614,6 +952,35 @@ int out_proj_check(const void* o, const void* W_o, const void* y, int B, int K, 
     return GDN_OK;
 }
 
+// Argument checks of the tiled decode step (B > kStepSkinnyMaxB).
+int tile_step_check(const void* x, const void* gamma, const void* W_qkvab, const void* conv_w_qkv,
+                    const void* cache_q, const void* cache_k, const void* cache_v, const void* xn_hist,
+                    const void* q, const void* k, const void* v, const void* a, const void* b, const void* o,
+                    const void* W_o, const void* y, int B, int D, int H, int dk, int dv, int conv_k) {
+    using gdn_host::aligned;
+    using gdn_host::fail;
+    if (D <= 0 || H <= 0 || dk <= 0 || dv <= 0)
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_step: D=%d H=%d dk=%d dv=%d", D, H, dk, dv);
+    if (D % kTlK != 0 || D > 16384)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_step: D=%d must be a multiple of %d, at most 16384", D, kTlK);
+    if ((H * dk) % kTlN != 0 || (H * dv) % kTlN != 0)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_step: H dk=%d and H dv=%d must be multiples of %d for B > %d",
+                    H * dk, H * dv, kTlN, kStepSkinnyMaxB);
+    if (conv_k < 1 || conv_k > 4) return fail(GDN_ERR_UNSUPPORTED, "decode_step: conv_k=%d must be in 1..4", conv_k);
+    // 32-bit byte offsets into x_n (bf16) and o (fp32)
+    if (static_cast<size_t>(B) * std::max(D, H * dv) * 4 > 0xFFFFFFFFull)
+        return fail(GDN_ERR_UNSUPPORTED, "decode_step: B=%d rows of D=%d / H dv=%d exceed 4 GiB", B, D, H * dv);
+    if (B == 0) return GDN_OK;
+    if (!x || !gamma || !W_qkvab || !conv_w_qkv || !q || !k || !v || !a || !b || !o || !W_o || !y ||
+        (conv_k > 1 && (!cache_q || !cache_k || !cache_v)))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_step: null pointer argument");
+    if (!aligned(x, 16) || !aligned(gamma, 16) || !aligned(W_qkvab, 16) || !aligned(W_o, 16) || !aligned(y, 16) ||
+        !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16) || !aligned(xn_hist, 16) ||
+        !aligned(cache_q, 16) || !aligned(cache_k, 16) || !aligned(cache_v, 16))
+        return fail(GDN_ERR_INVALID_ARGUMENT, "decode_step: x/gamma/W/W_o/y/q/k/v/o/caches/xn_hist need 16-byte alignment");
+    return GDN_OK;
+}
+
 }  // namespace
 
 extern "C" int gdn_decode_in_proj_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps,
@@ -674,19 +1041,61 @@ extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* 
     // Every stage's arguments are checked before the first launch: the
     // in-projection updates the conv caches and x_n history in place, so a
     // later stage refusing its arguments would leave the state half-advanced.
-    // Up to kStepMaxB sequences run as groups of kSkM: one in- and one
+    // Up to kStepSkinnyMaxB sequences run as groups of kSkM: one in- and one
     // out-projection launch per group (each streams the weights once more),
     // one recurrence launch for all; the groups' row offsets keep every
     // pointer's alignment, so checking the first group covers them all.
+    // Larger batches run RMSNorm (x_n into y, the x_n history shifted), the
+    // tiled in-projection, the recurrence and the tiled out-projection.
     if (B < 0 || B > kStepMaxB)
         return gdn_host::fail(B < 0 ? GDN_ERR_INVALID_ARGUMENT : GDN_ERR_UNSUPPORTED,
                               "decode_step: B=%d, at most %d sequences", B, kStepMaxB);
+    const bool tiled = B > kStepSkinnyMaxB;
     const int B0 = std::min(B, kSkM);
-    int st = in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B0, D, H, dk, dv,
-                           conv_k);
+    int st = tiled ? tile_step_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v, a,
+                                     b, o, W_o, y, B, D, H, dk, dv, conv_k)
+                   : in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B0, D, H,
+                                   dk, dv, conv_k);
     if (st == GDN_OK) st = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
-    if (st == GDN_OK) st = out_proj_check(o, W_o, y, B0, H * dv, D);
+    if (st == GDN_OK && !tiled) st = out_proj_check(o, W_o, y, B0, H * dv, D);
     if (st != GDN_OK || B == 0) return st;
+    if (tiled) {
+        hipStream_t hs = static_cast<hipStream_t>(stream);
+        st = gdn_host::rmsnorm_launch(x, gamma, y, xn_hist, xn_hist ? conv_k - 1 : 0, B, D, eps, hs);
+        if (st != GDN_OK) return st;
+        const int Hk = H * dk, Hv = H * dv;
+        TileParams p = {};
+        p.W = W_qkvab;
+        p.B = B;
+        p.K = D;
+        p.N = 2 * Hk + Hv + 2 * H;
+        p.xn = y;
+        p.conv_w = conv_w_qkv;
+        p.conv_k = conv_k;
+        p.cache[0] = cache_q;
+        p.cache[1] = cache_k;
+        p.cache[2] = cache_v;
+        uint16_t* dst[5] = {q, k, v, a, b};
+        const int col0[5] = {0, Hk, 2 * Hk, 2 * Hk + Hv, 2 * Hk + Hv + H};
+        const int width[5] = {Hk, Hk, Hv, H, H};
+        for (int i = 0; i < 5; ++i) {
+            p.dst[i] = dst[i];
+            p.col0[i] = col0[i];
+            p.width[i] = width[i];
+        }
+        st = launch_tile<0>(p, hs, "gdn_decode_tile_kernel<in>");
+        if (st != GDN_OK) return st;
+        st = gdn_decode_hip(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, S_out, B, H, dk, dv, stream);
+        if (st != GDN_OK) return st;
+        TileParams po = {};
+        po.W = W_o;
+        po.B = B;
+        po.K = Hv;
+        po.N = D;
+        po.o = o;
+        po.y = y;
+        return launch_tile<1>(po, hs, "gdn_decode_tile_kernel<out>");
+    }
     const int nc = conv_k - 1;
     const size_t Hk = static_cast<size_t>(H) * dk, Hv = static_cast<size_t>(H) * dv;
     auto off = [](auto* ptr, size_t n) { return ptr ? ptr + n : ptr; };

@@ -6,6 +6,10 @@
 // Here one wave64 owns a row; each lane moves 16-byte chunks (8 bf16), the
 // row stays in VGPRs between the sum of squares and the scaling, so x is read
 // once and y written once.  Four rows per 256-thread workgroup.
+//
+// The decode step's launch (gdn_host::rmsnorm_launch with a history) also
+// moves the row's x_n history [R, nc, D] one token older and appends y: each
+// lane shifts the chunks it owns, so the update is in place.
 #include "gdn_common.hpp"
 
 namespace {
@@ -16,12 +20,27 @@ using namespace gdn;
 template <int CHUNKS>  // 16-byte chunks per lane
 __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ gamma,
-                                                          uint16_t* __restrict__ y, int R, int D, float eps) {
+                                                          uint16_t* __restrict__ y, int R, int D, float eps,
+                                                          uint16_t* __restrict__ hist, int nc) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= R) return;
     const int nch = D >> 3;
     const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * D);
+    u32x4* const hrow = hist ? reinterpret_cast<u32x4*>(hist + static_cast<size_t>(row) * nc * D) : nullptr;
+    // History entries 1 .. nc - 1 (nc <= 3) of the lane's chunks load with x,
+    // so the shift below does not wait for a load per store.
+    constexpr bool kHoldHist = CHUNKS <= 8;
+    u32x4 hv[kHoldHist ? CHUNKS : 1][2];
+    if (kHoldHist && hrow) {
+#pragma unroll
+        for (int u = 0; u < (kHoldHist ? CHUNKS : 1); ++u) {
+            const int c = lane + 64 * u;
+#pragma unroll
+            for (int j = 1; j < 3; ++j)
+                if (j < nc && c < nch) hv[u][j - 1] = hrow[j * nch + c];
+        }
+    }
     u32x4 xv[CHUNKS];
     float ss = 0.f;
 #pragma unroll
@@ -49,11 +68,41 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __rest
                 o[e] = pack2_bf16((f[2 * e] * inv) * gm[2 * e], (f[2 * e + 1] * inv) * gm[2 * e + 1]);
             }
             yr[c] = o;
+            if (hrow) {
+                u32x4* const h = hrow + c;
+                if constexpr (kHoldHist) {
+                    if (nc > 1) h[0] = hv[u][0];
+                    if (nc > 2) h[nch] = hv[u][1];
+                } else {
+                    for (int j = 0; j + 1 < nc; ++j) h[j * nch] = h[(j + 1) * nch];
+                }
+                h[(nc - 1) * nch] = o;
+            }
         }
     }
 }
 
 }  // namespace
+
+int gdn_host::rmsnorm_launch(const void* x, const void* gamma, void* y, void* hist, int nc, int R, int D, float eps,
+                             hipStream_t s) {
+    if (nc < 0 || nc > 3) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "rmsnorm: history of %d tokens, at most 3", nc);
+    const dim3 grid((R + 3) / 4), block(256);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* gp = static_cast<const uint16_t*>(gamma);
+    auto* yp = static_cast<uint16_t*>(y);
+    auto* hp = nc > 0 ? static_cast<uint16_t*>(hist) : nullptr;
+    const int nch = D / 8;
+    if (nch <= 64 * 4)
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<4>, grid, block, 0, s, xp, gp, yp, R, D, eps, hp, nc);
+    else if (nch <= 64 * 8)
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<8>, grid, block, 0, s, xp, gp, yp, R, D, eps, hp, nc);
+    else if (nch <= 64 * 16)
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<16>, grid, block, 0, s, xp, gp, yp, R, D, eps, hp, nc);
+    else
+        hipLaunchKernelGGL(gdn_rmsnorm_kernel<32>, grid, block, 0, s, xp, gp, yp, R, D, eps, hp, nc);
+    return gdn_host::check_launch("gdn_rmsnorm_kernel");
+}
 
 extern "C" int gdn_rmsnorm_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, gdn_bf16_t* y, int R, int D,
                                float eps, void* stream) {
@@ -65,16 +114,5 @@ extern "C" int gdn_rmsnorm_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, gdn
     if (!x || !gamma || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "rmsnorm: null pointer argument");
     if (!aligned(x, 16) || !aligned(gamma, 16) || !aligned(y, 16))
         return fail(GDN_ERR_INVALID_ARGUMENT, "rmsnorm: buffers need 16-byte alignment");
-    const dim3 grid((R + 3) / 4), block(256);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int nch = D / 8;
-    if (nch <= 64 * 4)
-        hipLaunchKernelGGL(gdn_rmsnorm_kernel<4>, grid, block, 0, s, x, gamma, y, R, D, eps);
-    else if (nch <= 64 * 8)
-        hipLaunchKernelGGL(gdn_rmsnorm_kernel<8>, grid, block, 0, s, x, gamma, y, R, D, eps);
-    else if (nch <= 64 * 16)
-        hipLaunchKernelGGL(gdn_rmsnorm_kernel<16>, grid, block, 0, s, x, gamma, y, R, D, eps);
-    else
-        hipLaunchKernelGGL(gdn_rmsnorm_kernel<32>, grid, block, 0, s, x, gamma, y, R, D, eps);
-    return gdn_host::check_launch("gdn_rmsnorm_kernel");
+    return gdn_host::rmsnorm_launch(x, gamma, y, nullptr, 0, R, D, eps, static_cast<hipStream_t>(stream));
 }

@@ -116,9 +116,13 @@ class GDNLayerCustom:
         self.dt_bias_vec = _dt_bias_for_decode(dtb, self.H).float().contiguous()
         self.W_o = w['W_o'].contiguous()
         self.gamma = w['norm_gamma'].contiguous()
-        # Fused decode step (B <= 48): skinny input and output projections.
-        self.fused_decode = (self.D % 32 == 0 and self.D <= 4096 and (self.H * self.DV) % 32 == 0
-                             and self.H * self.DV <= 4096 and 1 <= self.CK <= 4)
+        # Fused decode step: skinny projections for B <= 48 (groups of 16
+        # sequences), 64 x 64 MFMA tiles above.
+        Hk, Hv = self.H * self.DK, self.H * self.DV
+        self.fused_decode = (self.D % 32 == 0 and self.D <= 4096 and Hv % 32 == 0
+                             and Hv <= 4096 and 1 <= self.CK <= 4)
+        self.tiled_decode = (self.D % 64 == 0 and self.D <= 16384 and Hk % 64 == 0 and Hv % 64 == 0
+                             and 1 <= self.CK <= 4)
 
     def init_decode_state(self, B, device=None):
         return _zero_decode_state(self.w, B, device=device)
@@ -248,10 +252,9 @@ class GDNLayerCustom:
         else:
             cq, ck, cv = (state[n].clone() for n in ('conv_q', 'conv_k', 'conv_v'))
             S_out = torch.empty_like(state['recurrent'])
-        # the fused step as groups of 16 sequences up to 48 (measured at
-        # config 5: 47 us at B=32 against 76 for the library-GEMM path; at
-        # B=64 the four groups' weight streams cost more: 93 against 77 us)
-        fused = self.fused_decode and B <= 48
+        # the fused step: groups of 16 sequences up to 48 (measured at config
+        # 5: 47 us at B=32 against 76 for the library-GEMM path), tiles above
+        fused = (self.fused_decode and B <= 48) or (self.tiled_decode and 48 < B <= 65535)
         if fused:
             # The whole step in one host call: RMSNorm + projections + conv
             # step + x_n history, the recurrence, the output projection.

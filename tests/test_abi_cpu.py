@@ -140,8 +140,21 @@ def test_decode_conv_step_validation_errors():
 def test_decode_step_validation_errors():
     """The fused step checks every stage's arguments before its first launch."""
     step_args = lambda B, D, dv: ([FAKE, FAKE, 1e-6] + [FAKE] * 10 + [0.1] + [FAKE] * 8 + [B, D, 2, 128, dv, 4, None])
-    with pytest.raises(GdnError, match="decode_step: B=65, at most 64"):
-        abi.call("gdn_layer_decode_step_hip", *step_args(65, 2048, 128))
+    with pytest.raises(GdnError, match="decode_step: B=65536, at most 65535"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(65536, 2048, 128))
+    # B > 48: the tiled path's own checks
+    with pytest.raises(GdnError, match="decode_step: D=100 must be a multiple of 64"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(65, 100, 128))
+    with pytest.raises(GdnError, match="decode_step: H dk=256 and H dv=32 must be multiples of 64"):
+        abi.call("gdn_layer_decode_step_hip", *step_args(65, 2048, 16))
+    tiled_misaligned = step_args(65, 2048, 128)
+    tiled_misaligned[21] = FAKE + 4  # y
+    with pytest.raises(GdnError, match="decode_step: x/gamma/W/W_o/y"):
+        abi.call("gdn_layer_decode_step_hip", *tiled_misaligned)
+    tiled_misaligned = step_args(65, 2048, 128)
+    tiled_misaligned[11] = FAKE + 4  # S_in: refused by the recurrence's checks, still before any launch
+    with pytest.raises(GdnError, match="decode: q/k/S/o need 16-byte"):
+        abi.call("gdn_layer_decode_step_hip", *tiled_misaligned)
     with pytest.raises(GdnError, match="decode_in_proj.*D=100"):
         abi.call("gdn_layer_decode_step_hip", *step_args(4, 100, 128))
     abi.call("gdn_layer_decode_step_hip", *step_args(0, 2048, 128))  # B == 0: no-op

@@ -82,14 +82,15 @@ def test_layer_decode_matches_prefill(dev, inplace):
     assert_out_close(torch.cat(ys, 1), y_pre, what="decode vs prefill")
 
 
-@pytest.mark.parametrize("B", [20, 40, 72])
+@pytest.mark.parametrize("B", [20, 40, 72, 130])
 def test_layer_decode_above_16_sequences_matches_prefill(dev, B):
     """17..48 sequences run the fused step as groups of 16 (B=20: a partial
-    second group; B=40: three groups), more take the unfused step (RMSNorm,
-    library GEMM, conv-step kernel, library GEMM); both must agree with one
-    prefill."""
+    second group; B=40: three groups), more the tiled step (B=72: a partial
+    second row tile; B=130: three row tiles, the last with 2 rows); both must
+    agree with one prefill."""
     _, w = _weights(dev, seed=9)
     layer = GDNLayerCustom(w)
+    assert layer.fused_decode and layer.tiled_decode
     x = torch.randn(B, 24, 256, generator=torch.Generator().manual_seed(10)).bfloat16().to(dev)
     y_pre = layer.forward(x)
     st = layer.init_decode_state(B)
@@ -98,6 +99,49 @@ def test_layer_decode_above_16_sequences_matches_prefill(dev, B):
         y_t, st = layer.decode(x[:, t:t + 1], st, inplace=True)
         ys.append(y_t)
     assert_out_close(torch.cat(ys, 1), y_pre, what=f"decode (B={B}) vs prefill")
+
+
+def test_layer_decode_unfused_path_matches_prefill(dev):
+    """The unfused step (RMSNorm, library GEMM, conv-step kernel, library GEMM),
+    which shapes outside the fused kernels take, against one prefill."""
+    _, w = _weights(dev, seed=9)
+    layer = GDNLayerCustom(w)
+    layer.tiled_decode = False
+    B = 72
+    x = torch.randn(B, 12, 256, generator=torch.Generator().manual_seed(10)).bfloat16().to(dev)
+    y_pre = layer.forward(x)
+    st = layer.init_decode_state(B)
+    ys = []
+    for t in range(12):
+        y_t, st = layer.decode(x[:, t:t + 1], st, inplace=True)
+        ys.append(y_t)
+    assert_out_close(torch.cat(ys, 1), y_pre, what="unfused decode vs prefill")
+
+
+@pytest.mark.parametrize("ck", [1, 2, 3])
+def test_layer_decode_tiled_conv_widths(dev, ck):
+    """The tiled step's conv epilogue at conv widths 1..3 (no cache, 1 or 2
+    cached tokens; width 4 is the default elsewhere): decode from a prefill's
+    state against one longer prefill, and the conv caches and x_n history."""
+    _, w = _weights(dev, seed=13)
+    w = dict(w)
+    for key in ("conv_q", "conv_k", "conv_v"):
+        w[key] = w[key][:, :ck].contiguous()
+    layer = GDNLayerCustom(w)
+    B = 66
+    x = torch.randn(B, 40, 256, generator=torch.Generator().manual_seed(14)).bfloat16().to(dev)
+    y_all, st_all = layer.forward(x, return_state=True)
+    _, st = layer.forward(x[:, :34], return_state=True)
+    ys = []
+    for t in range(34, 40):
+        y_t, st = layer.decode(x[:, t:t + 1], st)
+        ys.append(y_t)
+    assert_out_close(torch.cat(ys, 1), y_all[:, 34:], what=f"conv width {ck}: tiled decode vs prefill")
+    assert_state_close(st["recurrent"].cpu(), st_all["recurrent"].cpu())
+    for key in ("conv_q", "conv_k", "conv_v", "xn"):
+        assert st[key].shape == st_all[key].shape, key
+        if st[key].numel():
+            assert_out_close(st[key].cpu(), st_all[key].cpu(), what=key)
 
 
 def test_prefill_hands_off_to_decode(dev):
@@ -117,15 +161,17 @@ def test_prefill_hands_off_to_decode(dev):
     assert_out_close(torch.cat([y_a, y_b], 1), y_full, what="prefill + prefill vs prefill")
 
 
-def test_layer_decode_graph_replays_match_eager(dev):
-    """capture_decode: one decode step as a HIP graph.  Every replay (with eager
-    work and a synchronisation between replays) must give the eager step's
-    output and state: the captured chain holds no memset nodes and reads the
-    state dict's tensors in place."""
+@pytest.mark.parametrize("B", [3, 72])
+def test_layer_decode_graph_replays_match_eager(dev, B):
+    """capture_decode: one decode step as a HIP graph (B=3: the skinny fused
+    step, B=72: the tiled one).  Every replay (with eager work and a
+    synchronisation between replays) must give the eager step's output and
+    state: the captured chain holds no memset nodes and reads the state
+    dict's tensors in place."""
     w_cpu, w = _weights(dev, seed=3)
     layer = GDNLayerCustom(w)
     g = torch.Generator().manual_seed(4)
-    x = torch.randn(3, 70, 256, generator=g).bfloat16().to(dev)
+    x = torch.randn(B, 70, 256, generator=g).bfloat16().to(dev)
     _, st = layer.forward(x, return_state=True)
     st_eager = {k: v.clone() for k, v in st.items()}
     st_graph = {k: v.clone() for k, v in st.items()}
@@ -133,7 +179,7 @@ def test_layer_decode_graph_replays_match_eager(dev):
     for k in st:  # capture leaves the state as it was
         assert torch.equal(st_graph[k], st_eager[k]), k
     for i in range(6):
-        xt = torch.randn(3, 1, 256, generator=g).bfloat16().to(dev)
+        xt = torch.randn(B, 1, 256, generator=g).bfloat16().to(dev)
         y_e, st_eager = layer.decode(xt, st_eager, inplace=True)
         y_g = step(xt).clone()
         torch.cuda.synchronize()
@@ -199,14 +245,14 @@ def test_layer_config5_decode_after_prefill(dev):
         assert_out_close(st[key].cpu(), st_all[key].cpu(), what=key)
 
 
-@pytest.mark.parametrize("B", [4, 20, 72])
+@pytest.mark.parametrize("B", [4, 20, 72, 130])
 def test_layer_config5_decode_matches_oracle(dev, B):
     """Config-5 dims: a GPU prefill (T=192) hands its decode state to both the
     GPU layer and the oracle layer's decode (fp32 projection); four steps on
     each, compared step by step (outputs to the scaled 2e-2 bar), then the
     recurrent state (1e-2 relative), conv caches and x_n history.  B=4 runs
-    the fused decode step, B=20 the fused step as two groups, B=72 the
-    unfused one (library GEMMs)."""
+    the fused decode step, B=20 the fused step as two groups, B=72 and B=130
+    the tiled step (two and three row tiles)."""
     g, w_cpu, w = _cfg5_weights(dev, seed=12)
     layer, base = GDNLayerCustom(w), GDNLayerBaseline(w_cpu, fp32_proj=True)
     x = torch.randn(B, 196, 2048, generator=g).bfloat16()
