@@ -12,12 +12,13 @@ Pipeline per call (all GPU, one stream):
            (and, on request, the conv cache for decode) -> chunked prefill
            (output written token-major) -> W_o GEMM.  No .item() host sync: dt_bias is read once at
            construction (call ``refresh()`` after changing the weights).
-  decode   one host call per step (B <= 48, as groups of 16 sequences): the
+  decode   one host call per step.  B <= 48, as groups of 16 sequences: the
            fused RMSNorm + q/k/v/a/b projection + conv step kernel, the decode
            kernel (state update in place when asked) and the W_o projection
-           kernel.  Larger batches:
-           RMSNorm kernel -> xn W^T GEMM -> decode conv step -> decode kernel
-           -> W_o GEMM.
+           kernel.  Larger batches: RMSNorm kernel (+ x_n history) -> tiled
+           in-projection with the conv step in its epilogue -> decode kernel
+           -> tiled W_o projection.  Shapes outside both: RMSNorm kernel ->
+           xn W^T GEMM -> decode conv step -> decode kernel -> W_o GEMM.
 
 The baseline (pure PyTorch) layer of the reference is the oracle's
 ``oracle.layer_ref.GDNLayerBaseline``; it is test infrastructure, not shipped.
@@ -238,9 +239,9 @@ class GDNLayerCustom:
         tokens (the reference baseline's decode semantics).  With
         ``inplace=True`` the state tensors are updated in place and the same
         dict is returned (no allocation of a new 4-D state per step).
-        The fused step (B <= 48) keeps its q/k/v/a/b/o intermediates per
-        (batch size, device, stream), so concurrent decodes of one layer must
-        run on different streams (or different batch sizes).
+        The fused step keeps its q/k/v/a/b/o intermediates per (batch size,
+        device, stream), so concurrent decodes of one layer must run on
+        different streams (or different batch sizes).
         """
         B, T, _ = x.shape
         assert T == 1, f"decode expects T=1, got T={T}"

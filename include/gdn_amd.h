@@ -305,11 +305,16 @@ int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W, gdn_bf16_t* y, 
  * in place when S_out == S_in) and gdn_decode_out_proj_hip, so a serving loop
  * pays one host call per step.  q, k, v, a, b ([B, H dk] x2, [B, H dv],
  * [B, H] x2 bf16) and o ([B, H dv] fp32) are caller-owned scratch; y is
- * [B, D] bf16.  B <= 64: the projections run as groups of 16 sequences (one
+ * [B, D] bf16.  B <= 48: the projections run as groups of 16 sequences (one
  * gdn_decode_in_proj_hip and one gdn_decode_out_proj_hip launch per group),
- * the recurrence once for all B.  Other constraints and errors are those of
- * the three entry points; every argument is checked before the first launch,
- * so a refused call leaves the caches and state untouched.
+ * the recurrence once for all B; other constraints and errors are those of
+ * the three entry points.  48 < B <= 65535: RMSNorm (x_n written to y, which
+ * is then scratch until the out-projection overwrites it, and the x_n
+ * history shifted), a tiled in-projection with the conv step in its
+ * epilogue, the recurrence, a tiled out-projection; D % 64 == 0, D <= 16384,
+ * H dk and H dv multiples of 64, conv_k in 1..4, x/gamma/W/W_o/y/q/k/v/o/
+ * caches/xn_hist 16-byte aligned.  Every argument is checked before the first
+ * launch, so a refused call leaves the caches and state untouched.
  * Replaces GDNLayerCustom.decode (gdn_layer.py:265-316) as a whole.
  */
 int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* gamma, float eps, const gdn_bf16_t* W_qkvab,
