@@ -173,10 +173,9 @@ def serve_leg(exts, dev, cpu, nthr, torch):
     """GDNLayerCustom.decode at B in {1, 8, 32, 64, 128, 256}, config-5 dims (the
     reference's layer decode sweep, bench_gdn.py:332-342): one step = RMSNorm,
     q/k/v/a/b projection + conv step, the recurrence (state in place), W_o.
-    B <= 48 runs the fused step with the skinny projection kernels (groups of
-    16 sequences), larger B the fused step with the tiled projection kernels
-    (RMSNorm, tiled in-projection + conv step, recurrence, tiled
-    out-projection).  Roofline: HBM, algorithmic bytes per step = both
+    B <= 16 runs the fused step with the skinny projection kernels, larger B
+    the fused step with the tiled projection kernels (RMSNorm, tiled
+    in-projection + conv step, recurrence, tiled out-projection).  Roofline: HBM, algorithmic bytes per step = both
     weight matrices + the fp32 state read and written + x in and y out.
     Parity at B=256: two steps from the same state against the oracle layer's
     decode (fp32 projection), which is also the CPU baseline."""
@@ -213,8 +212,8 @@ def serve_leg(exts, dev, cpu, nthr, torch):
         leg[f"B{SB}"] = {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "tokens_per_s": SB * 1e3 / ms,
                          "gbs": nbytes / (ms * 1e6), "hbm_frac": nbytes / (ms * 1e6) / PEAK_HBM_GBS,
                          "bytes": nbytes,
-                         "path": ("fused step (skinny projections)" if SB <= 48 and layer.fused_decode else
-                                  "fused step (tiled projections)" if SB > 48 and layer.tiled_decode else "unfused")}
+                         "path": ("fused step (skinny projections)" if SB <= 16 and layer.fused_decode else
+                                  "fused step (tiled projections)" if SB > 16 and layer.tiled_decode else "unfused")}
         log(f"layer decode B={SB}: {ms * 1e3:.1f} us/step, {nbytes / (ms * 1e6):.0f} GB/s")
         del st, xs
     # parity and CPU baseline at B=256

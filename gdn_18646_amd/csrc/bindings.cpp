@@ -531,7 +531,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     ml.def("decode_out_proj", &decode_out_proj, "Decode step output projection (B <= 16): bf16(o) W^T",
            py::arg("o"), py::arg("W"));
     ml.def("decode_step", &decode_step,
-           "Whole decode step (B <= 48: skinny projections in groups of 16; larger B: tiled projections): in-projection, "
+           "Whole decode step (B <= 16: skinny projections; larger B: tiled projections): in-projection, "
            "recurrence, out-projection in one call; caches, xn_hist and S_out updated in place, y written; q, k, v, a, b, "
            "o are scratch",
            py::arg("x"), py::arg("gamma"), py::arg("eps"), py::arg("W_qkvab"), py::arg("conv_w_qkv"),

@@ -48,7 +48,9 @@ constexpr int kRowsPerWave = kDK / kWavesPerWG;
 // CU's 160 KiB and a third does not.
 constexpr int kRedSlots = 72 * 1024 / 16;
 
-template <int CW>
+// OBF16: o is written as bf16 (round to nearest even of the fp32 value) into
+// a [B, H, dv] bf16 buffer, for the decode step's out-projection.
+template <int CW, bool OBF16>
 __global__ __launch_bounds__(kWave* kWavesPerWG) void gdn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ a,
@@ -128,7 +130,11 @@ __global__ __launch_bounds__(kWave* kWavesPerWG) void gdn_decode_kernel(
         f32x4 ot = red[kWavesPerWG * LPR + c];
 #pragma unroll
         for (int w = 1; w < kWavesPerWG; ++w) ot += red[(kWavesPerWG + w) * LPR + c];
-        *reinterpret_cast<f32x4*>(o + static_cast<size_t>(bh) * dv + col) = scale * ot;
+        if constexpr (OBF16)
+            *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(o) + static_cast<size_t>(bh) * dv + col) =
+                pack4_bf16(scale * ot);
+        else
+            *reinterpret_cast<f32x4*>(o + static_cast<size_t>(bh) * dv + col) = scale * ot;
     }
 }
 
@@ -154,13 +160,9 @@ int decode_check(const void* q, const void* k, const void* v, const void* a, con
 
 }  // namespace gdn_host
 
-extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
-                              const gdn_bf16_t* a, const gdn_bf16_t* b, const float* A_log,
-                              const float* dt_bias, const float* S_in, float scale, float* o,
-                              float* S_out, int B, int H, int dk, int dv, void* stream) {
-    using gdn_host::fail;
-    const int chk = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
-    if (chk != GDN_OK || B == 0) return chk;
+int gdn_host::decode_launch(const void* q, const void* k, const void* v, const void* a, const void* b,
+                           const float* A_log, const float* dt_bias, const float* S_in, float scale, void* o,
+                           bool o_bf16, float* S_out, int B, int H, int dv, hipStream_t st) {
     // Column slice: the widest of 128 / 64 / 32 dividing dv, halved while the
     // grid would leave CUs idle (a small batch splits each head's columns
     // over more workgroups; columns of the state update independently).
@@ -170,15 +172,30 @@ extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gd
     const long long nwg_ll = static_cast<long long>(B) * H * (dv / cw);
     if (nwg_ll > 0x7fffffffLL) return fail(GDN_ERR_UNSUPPORTED, "decode: grid too large");
     const dim3 grid(static_cast<unsigned>(nwg_ll)), block(kWave * kWavesPerWG);
-    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* qp = static_cast<const uint16_t*>(q);
+    const auto* kp = static_cast<const uint16_t*>(k);
+    const auto* vp = static_cast<const uint16_t*>(v);
+    const auto* ap = static_cast<const uint16_t*>(a);
+    const auto* bp = static_cast<const uint16_t*>(b);
+    auto* op = static_cast<float*>(o);
+    auto launch = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, 0, st, qp, kp, vp, ap, bp, A_log, dt_bias, S_in, scale, op, S_out, H, dv);
+    };
     if (cw == 128)
-        hipLaunchKernelGGL(gdn_decode_kernel<128>, grid, block, 0, st, q, k, v, a, b, A_log, dt_bias, S_in, scale, o,
-                           S_out, H, dv);
+        o_bf16 ? launch(gdn_decode_kernel<128, true>) : launch(gdn_decode_kernel<128, false>);
     else if (cw == 64)
-        hipLaunchKernelGGL(gdn_decode_kernel<64>, grid, block, 0, st, q, k, v, a, b, A_log, dt_bias, S_in, scale, o,
-                           S_out, H, dv);
+        o_bf16 ? launch(gdn_decode_kernel<64, true>) : launch(gdn_decode_kernel<64, false>);
     else
-        hipLaunchKernelGGL(gdn_decode_kernel<32>, grid, block, 0, st, q, k, v, a, b, A_log, dt_bias, S_in, scale, o,
-                           S_out, H, dv);
+        o_bf16 ? launch(gdn_decode_kernel<32, true>) : launch(gdn_decode_kernel<32, false>);
     return gdn_host::check_launch("gdn_decode_kernel");
+}
+
+extern "C" int gdn_decode_hip(const gdn_bf16_t* q, const gdn_bf16_t* k, const gdn_bf16_t* v,
+                              const gdn_bf16_t* a, const gdn_bf16_t* b, const float* A_log,
+                              const float* dt_bias, const float* S_in, float scale, float* o,
+                              float* S_out, int B, int H, int dk, int dv, void* stream) {
+    const int chk = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
+    if (chk != GDN_OK || B == 0) return chk;
+    return gdn_host::decode_launch(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, false, S_out, B, H, dv,
+                                   static_cast<hipStream_t>(stream));
 }

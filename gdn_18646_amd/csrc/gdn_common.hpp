@@ -195,6 +195,12 @@ inline bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_
 int decode_check(const void* q, const void* k, const void* v, const void* a, const void* b, const void* A_log,
                  const void* dt_bias, const void* S_in, const void* o, const void* S_out, int B, int H, int dk,
                  int dv);
+// The decode recurrence launch behind gdn_decode_hip (defined in decode.hip;
+// arguments already checked by decode_check).  o_bf16: o is written as bf16
+// [B, H, dv] (RNE of the fp32 value) into the buffer o points to.
+int decode_launch(const void* q, const void* k, const void* v, const void* a, const void* b, const float* A_log,
+                  const float* dt_bias, const float* S_in, float scale, void* o, bool o_bf16, float* S_out, int B,
+                  int H, int dv, hipStream_t stream);
 // RMSNorm of R rows (defined in rmsnorm.hip; arguments already checked as
 // gdn_rmsnorm_hip checks them).  hist (nc > 0): the rows' x_n history
 // [R, nc, D] (nc <= 3), shifted one token older with y appended, in place.

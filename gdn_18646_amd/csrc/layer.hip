@@ -106,7 +106,6 @@ constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkMaxCols = 16;  // weight rows (output columns) per workgroup: 16, or 8 to spread small N
 constexpr int kSkStride = 32 * kSkWaves;  // K elements between a wave's consecutive steps
 constexpr int kSkCUs = 256;
-constexpr int kStepSkinnyMaxB = 48;  // gdn_layer_decode_step_hip: up to here groups of kSkM, above it tiles
 constexpr int kStepMaxB = 65535;     // gdn_layer_decode_step_hip: sequences
 
 struct SkinnyParams {
@@ -383,11 +382,16 @@ int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
 // sit in 1 KB blocks with their 16-byte chunks XOR-swizzled, so the 16 lanes
 // of an operand read (16 rows, one chunk) hit 16 different bank groups.
 //
+// The loop keeps the ring full: slice i's MFMAs run on fragments read from
+// LDS during the previous iteration, while slice i + 1's fragments are read,
+// and slice i's slot is refilled as soon as its fragments are in registers.
+//
 // MODE 0, the in-projection: A = x_n [B, K] bf16, W = [W_q; W_k; W_v; W_a;
 // W_b].  P = x_n W^T stays fp32 for the conv step (as in the skinny kernel):
 // q/k/v take SiLU(conv over the cached tokens and P), their caches shift one
 // token in place, a and b take P.  MODE 1, the out-projection: A = o [B, K]
-// fp32, rounded to bf16 as the MFMA operand is built; y = bf16(o W_o^T).
+// as bf16 (the recurrence writes it rounded to nearest even, the rounding of
+// the reference's o.to(bf16)); y = bf16(o W_o^T).
 // ---------------------------------------------------------------------------
 constexpr int kTlM = 64;    // sequences per tile
 constexpr int kTlN = 64;    // weight rows (output columns) per tile
@@ -401,8 +405,7 @@ struct TileParams {
     const uint16_t* W;       // [N, K]
     int B, K, N;
     int mtiles, ntiles;
-    const uint16_t* xn;      // MODE 0: x_n [B, K] bf16
-    const float* o;          // MODE 1: o [B, K] fp32
+    const uint16_t* A;       // [B, K] bf16: x_n (MODE 0) or o (MODE 1)
     uint16_t* y;             // MODE 1: y [B, N] bf16
     const uint16_t* conv_w;  // MODE 0: [2 H dk + H dv, conv_k]
     int conv_k;
@@ -414,7 +417,7 @@ struct TileParams {
 
 template <int MODE>
 struct TileCfg {
-    static constexpr int kABytes = kTlM * kTlK * (MODE == 0 ? 2 : 4);  // A slice of one stage
+    static constexpr int kABytes = kTlM * kTlK * 2;  // A slice of one stage
     static constexpr int kBBytes = kTlN * kTlK * 2;
     static constexpr int kStageBytes = kABytes + kBBytes;
     static constexpr int kStages = 4;
@@ -428,13 +431,10 @@ struct TileCfg {
     static_assert(kADma >= 1 && kBDma >= 1, "every wave issues whole 1 KB blocks");
 };
 
-// Byte offset in a stage of (row r, 16-byte chunk c) of a bf16 slice (8
-// chunks a row, 8 rows a KB) and of an fp32 slice (16 chunks, 4 rows a KB).
-__device__ __forceinline__ uint32_t tl_off_bf16(int r, int c) {
+// Byte offset in a stage of (row r, 16-byte chunk c) of a slice: 8 chunks a
+// row, 8 rows a KB.
+__device__ __forceinline__ uint32_t tl_off(int r, int c) {
     return (r >> 3) * 1024 + (r & 7) * 128 + ((c ^ ((r >> 1) & 7)) << 4);
-}
-__device__ __forceinline__ uint32_t tl_off_f32(int r, int c) {
-    return (r >> 2) * 1024 + (r & 3) * 256 + ((c ^ (r & 15)) << 4);
 }
 
 template <int N>
@@ -502,7 +502,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     }
 
     // DMA source offsets (bytes from the slice's first K column) of this
-    // lane's chunk in each of its 1 KB blocks.
+    // lane's chunk in its 1 KB blocks of A and of W.
     const uint16_t* const Wt = p.W + static_cast<size_t>(n0) * p.K;
     uint32_t aoff[Cfg::kADma], boff[Cfg::kBDma];
 #pragma unroll
@@ -513,26 +513,15 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     }
 #pragma unroll
     for (int u = 0; u < Cfg::kADma; ++u) {
-        if constexpr (MODE == 0) {
-            const int r = 8 * (wave + kTlWaves * u) + (lane >> 3);
-            const int c = (lane & 7) ^ ((r >> 1) & 7);
-            aoff[u] = static_cast<uint32_t>(min(m0 + r, p.B - 1) * p.K + 8 * c) * 2;
-        } else {
-            const int r = 4 * (wave + kTlWaves * u) + (lane >> 4);
-            const int c = (lane & 15) ^ (r & 15);
-            aoff[u] = static_cast<uint32_t>(min(m0 + r, p.B - 1) * p.K + 4 * c) * 4;
-        }
+        const int r = 8 * (wave + kTlWaves * u) + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        aoff[u] = static_cast<uint32_t>(min(m0 + r, p.B - 1) * p.K + 8 * c) * 2;
     }
     auto issue = [&](int ks, int slot) {
         lds_u8* const st = ring + slot * Cfg::kStageBytes;
         const int k0 = (ks + kstart < nk ? ks + kstart : ks + kstart - nk) * kTlK;
 #pragma unroll
-        for (int u = 0; u < Cfg::kADma; ++u) {
-            if constexpr (MODE == 0)
-                dma16(p.xn + k0, aoff[u], st + (wave + kTlWaves * u) * 1024);
-            else
-                dma16(p.o + k0, aoff[u], st + (wave + kTlWaves * u) * 1024);
-        }
+        for (int u = 0; u < Cfg::kADma; ++u) dma16(p.A + k0, aoff[u], st + (wave + kTlWaves * u) * 1024);
 #pragma unroll
         for (int u = 0; u < Cfg::kBDma; ++u) dma16(Wt + k0, boff[u], st + Cfg::kABytes + (wave + kTlWaves * u) * 1024);
     };
@@ -546,43 +535,51 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // The wave's A and W fragments of the slice in `slot`.
+    auto read_frags = [&](int slot, bf16x8* af, bf16x8* bw) {
+        const lds_u8* const sa = ring + slot * Cfg::kStageBytes;
+        const lds_u8* const sb = sa + Cfg::kABytes;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+            af[mi] = *reinterpret_cast<const lds_bf16x8*>(sa + tl_off(32 * wm + 16 * mi + r16, kc));
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+            bw[ni] = *reinterpret_cast<const lds_bf16x8*>(sb + tl_off(32 * wn + 16 * ni + r16, kc));
+    };
 
+    // Slices s go to slot s % S.  All S slots fill first; at iteration i
+    // slice i + 1 is waited for (the slices issued after it may fly), slice
+    // i's slot -- its fragments already in registers -- takes slice i + S,
+    // and slice i + 1's fragments are read while slice i's MFMAs run.
     constexpr int S = Cfg::kStages;
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s)
+    for (int s = 0; s < S; ++s)
         if (s < nk) issue(s, s);
+    if (S <= nk)
+        wait_vm<(S - 1) * Cfg::kDma>();
+    else
+        wait_vm<0>();
+    lds_barrier();
+    bf16x8 af[2], bw[2];
+    read_frags(0, af, bw);
     for (int i = 0; i < nk; ++i) {
-        // Slice i has landed when at most the S - 2 slices issued after it
-        // are in flight (fewer are issued near the end: wait for all).
-        if (i + S - 2 < nk)
+        // Slice i + 1 has landed when at most the S - 2 slices issued after
+        // it are in flight (fewer are issued near the end: wait for all).
+        if (i + S - 1 < nk)
             wait_vm<(S - 2) * Cfg::kDma>();
         else
             wait_vm<0>();
-        // Every wave's part of slice i is in LDS, and every wave is done
-        // with slice i - 1, whose slot the next issue refills.
+        // Every wave's part of slice i + 1 is in LDS, and every wave has
+        // slice i's fragments in registers (the barrier waits for its LDS
+        // reads), so slice i's slot is free.
         lds_barrier();
-        if (i + S - 1 < nk) issue(i + S - 1, (i + S - 1) % S);
-        const lds_u8* const sa = ring + (i % S) * Cfg::kStageBytes;
-        const lds_u8* const sb = sa + Cfg::kABytes;
-        bf16x8 af[2], bw[2];
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-            const int r = 32 * wm + 16 * mi + r16;
-            if constexpr (MODE == 0) {
-                af[mi] = *reinterpret_cast<const lds_bf16x8*>(sa + tl_off_bf16(r, kc));
-            } else {
-                const f32x4 lo = *reinterpret_cast<const lds_f32x4*>(sa + tl_off_f32(r, 2 * kc));
-                const f32x4 hi = *reinterpret_cast<const lds_f32x4*>(sa + tl_off_f32(r, 2 * kc + 1));
-                af[mi] = pack8(lo, hi);
-            }
-        }
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-            bw[ni] = *reinterpret_cast<const lds_bf16x8*>(sb + tl_off_bf16(32 * wn + 16 * ni + r16, kc));
+        if (i + S < nk) issue(i + S, i % S);
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma16x16x32(af[mi], bw[ni], acc[mi][ni]);
+        // slice i + 1's fragments (past the last slice: a valid slot, unused)
+        read_frags((i + 1) % S, af, bw);
     }
 
     // P tile [kTlM][kTlPitch] fp32 over the ring (every wave is past its
@@ -952,7 +949,7 @@ int out_proj_check(const void* o, const void* W_o, const void* y, int B, int K, 
     return GDN_OK;
 }
 
-// Argument checks of the tiled decode step (B > kStepSkinnyMaxB).
+// Argument checks of the tiled decode step (B > kSkM).
 int tile_step_check(const void* x, const void* gamma, const void* W_qkvab, const void* conv_w_qkv,
                     const void* cache_q, const void* cache_k, const void* cache_v, const void* xn_hist,
                     const void* q, const void* k, const void* v, const void* a, const void* b, const void* o,
@@ -965,7 +962,7 @@ int tile_step_check(const void* x, const void* gamma, const void* W_qkvab, const
         return fail(GDN_ERR_UNSUPPORTED, "decode_step: D=%d must be a multiple of %d, at most 16384", D, kTlK);
     if ((H * dk) % kTlN != 0 || (H * dv) % kTlN != 0)
         return fail(GDN_ERR_UNSUPPORTED, "decode_step: H dk=%d and H dv=%d must be multiples of %d for B > %d",
-                    H * dk, H * dv, kTlN, kStepSkinnyMaxB);
+                    H * dk, H * dv, kTlN, kSkM);
     if (conv_k < 1 || conv_k > 4) return fail(GDN_ERR_UNSUPPORTED, "decode_step: conv_k=%d must be in 1..4", conv_k);
     // 32-bit byte offsets into x_n (bf16) and o (fp32)
     if (static_cast<size_t>(B) * std::max(D, H * dv) * 4 > 0xFFFFFFFFull)
@@ -1041,23 +1038,21 @@ extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* 
     // Every stage's arguments are checked before the first launch: the
     // in-projection updates the conv caches and x_n history in place, so a
     // later stage refusing its arguments would leave the state half-advanced.
-    // Up to kStepSkinnyMaxB sequences run as groups of kSkM: one in- and one
-    // out-projection launch per group (each streams the weights once more),
-    // one recurrence launch for all; the groups' row offsets keep every
-    // pointer's alignment, so checking the first group covers them all.
-    // Larger batches run RMSNorm (x_n into y, the x_n history shifted), the
-    // tiled in-projection, the recurrence and the tiled out-projection.
+    // Up to kSkM sequences run the skinny projections around the recurrence;
+    // larger batches run RMSNorm (x_n into y, the x_n history shifted), the
+    // tiled in-projection, the recurrence and the tiled out-projection
+    // (measured at config 5: 33 against 38 us at B=17, 44 against 70 at
+    // B=48 for the skinny kernels in groups of 16).
     if (B < 0 || B > kStepMaxB)
         return gdn_host::fail(B < 0 ? GDN_ERR_INVALID_ARGUMENT : GDN_ERR_UNSUPPORTED,
                               "decode_step: B=%d, at most %d sequences", B, kStepMaxB);
-    const bool tiled = B > kStepSkinnyMaxB;
-    const int B0 = std::min(B, kSkM);
+    const bool tiled = B > kSkM;
     int st = tiled ? tile_step_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v, a,
                                      b, o, W_o, y, B, D, H, dk, dv, conv_k)
-                   : in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B0, D, H,
+                   : in_proj_check(x, gamma, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, q, k, v, a, b, B, D, H,
                                    dk, dv, conv_k);
     if (st == GDN_OK) st = gdn_host::decode_check(q, k, v, a, b, A_log, dt_bias, S_in, o, S_out, B, H, dk, dv);
-    if (st == GDN_OK && !tiled) st = out_proj_check(o, W_o, y, B0, H * dv, D);
+    if (st == GDN_OK && !tiled) st = out_proj_check(o, W_o, y, B, H * dv, D);
     if (st != GDN_OK || B == 0) return st;
     if (tiled) {
         hipStream_t hs = static_cast<hipStream_t>(stream);
@@ -1069,7 +1064,7 @@ extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* 
         p.B = B;
         p.K = D;
         p.N = 2 * Hk + Hv + 2 * H;
-        p.xn = y;
+        p.A = y;
         p.conv_w = conv_w_qkv;
         p.conv_k = conv_k;
         p.cache[0] = cache_q;
@@ -1085,36 +1080,22 @@ extern "C" int gdn_layer_decode_step_hip(const gdn_bf16_t* x, const gdn_bf16_t* 
         }
         st = launch_tile<0>(p, hs, "gdn_decode_tile_kernel<in>");
         if (st != GDN_OK) return st;
-        st = gdn_decode_hip(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, S_out, B, H, dk, dv, stream);
+        // o as bf16 in the first half of the caller's fp32 o buffer
+        st = gdn_host::decode_launch(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, true, S_out, B, H, dv, hs);
         if (st != GDN_OK) return st;
         TileParams po = {};
         po.W = W_o;
         po.B = B;
         po.K = Hv;
         po.N = D;
-        po.o = o;
+        po.A = reinterpret_cast<const uint16_t*>(o);
         po.y = y;
         return launch_tile<1>(po, hs, "gdn_decode_tile_kernel<out>");
     }
-    const int nc = conv_k - 1;
-    const size_t Hk = static_cast<size_t>(H) * dk, Hv = static_cast<size_t>(H) * dv;
-    auto off = [](auto* ptr, size_t n) { return ptr ? ptr + n : ptr; };
-    for (int r0 = 0; r0 < B; r0 += kSkM) {
-        const int Bg = std::min(kSkM, B - r0);
-        const size_t r = static_cast<size_t>(r0);
-        st = gdn_decode_in_proj_hip(x + r * D, gamma, eps, W_qkvab, conv_w_qkv, off(cache_q, r * Hk * nc),
-                                    off(cache_k, r * Hk * nc), off(cache_v, r * Hv * nc),
-                                    off(xn_hist, r * nc * D), q + r * Hk, k + r * Hk, v + r * Hv, a + r * H,
-                                    b + r * H, Bg, D, H, dk, dv, conv_k, stream);
-        if (st != GDN_OK) return st;
-    }
+    st = gdn_decode_in_proj_hip(x, gamma, eps, W_qkvab, conv_w_qkv, cache_q, cache_k, cache_v, xn_hist, q, k, v, a, b,
+                                B, D, H, dk, dv, conv_k, stream);
+    if (st != GDN_OK) return st;
     st = gdn_decode_hip(q, k, v, a, b, A_log, dt_bias, S_in, scale, o, S_out, B, H, dk, dv, stream);
     if (st != GDN_OK) return st;
-    for (int r0 = 0; r0 < B; r0 += kSkM) {
-        const int Bg = std::min(kSkM, B - r0);
-        const size_t r = static_cast<size_t>(r0);
-        st = gdn_decode_out_proj_hip(o + r * Hv, W_o, y + r * D, Bg, static_cast<int>(Hv), D, stream);
-        if (st != GDN_OK) return st;
-    }
-    return GDN_OK;
+    return gdn_decode_out_proj_hip(o, W_o, y, B, H * dv, D, stream);
 }

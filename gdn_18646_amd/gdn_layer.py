@@ -12,10 +12,10 @@ Pipeline per call (all GPU, one stream):
            (and, on request, the conv cache for decode) -> chunked prefill
            (output written token-major) -> W_o GEMM.  No .item() host sync: dt_bias is read once at
            construction (call ``refresh()`` after changing the weights).
-  decode   one host call per step.  B <= 48, as groups of 16 sequences: the
-           fused RMSNorm + q/k/v/a/b projection + conv step kernel, the decode
-           kernel (state update in place when asked) and the W_o projection
-           kernel.  Larger batches: RMSNorm kernel (+ x_n history) -> tiled
+  decode   one host call per step.  B <= 16: the fused RMSNorm + q/k/v/a/b
+           projection + conv step kernel, the decode kernel (state update in
+           place when asked) and the W_o projection kernel.  Larger batches:
+           RMSNorm kernel (+ x_n history) -> tiled
            in-projection with the conv step in its epilogue -> decode kernel
            -> tiled W_o projection.  Shapes outside both: RMSNorm kernel ->
            xn W^T GEMM -> decode conv step -> decode kernel -> W_o GEMM.
@@ -117,8 +117,8 @@ class GDNLayerCustom:
         self.dt_bias_vec = _dt_bias_for_decode(dtb, self.H).float().contiguous()
         self.W_o = w['W_o'].contiguous()
         self.gamma = w['norm_gamma'].contiguous()
-        # Fused decode step: skinny projections for B <= 48 (groups of 16
-        # sequences), 64 x 64 MFMA tiles above.
+        # Fused decode step: skinny projections for B <= 16, 64 x 64 MFMA
+        # tiles above.
         Hk, Hv = self.H * self.DK, self.H * self.DV
         self.fused_decode = (self.D % 32 == 0 and self.D <= 4096 and Hv % 32 == 0
                              and Hv <= 4096 and 1 <= self.CK <= 4)
@@ -253,9 +253,10 @@ class GDNLayerCustom:
         else:
             cq, ck, cv = (state[n].clone() for n in ('conv_q', 'conv_k', 'conv_v'))
             S_out = torch.empty_like(state['recurrent'])
-        # the fused step: groups of 16 sequences up to 48 (measured at config
-        # 5: 47 us at B=32 against 76 for the library-GEMM path), tiles above
-        fused = (self.fused_decode and B <= 48) or (self.tiled_decode and 48 < B <= 65535)
+        # the fused step: skinny projections up to 16 sequences, tiles above
+        # (config 5: 37 us at B=32, 123 at B=256, against 76 and 139 for the
+        # library-GEMM path)
+        fused = (self.fused_decode and B <= 16) or (self.tiled_decode and 16 < B <= 65535)
         if fused:
             # The whole step in one host call: RMSNorm + projections + conv
             # step + x_n history, the recurrence, the output projection.
@@ -268,7 +269,7 @@ class GDNLayerCustom:
             if inplace:
                 return y, state
             return y, dict(recurrent=S_out, conv_q=cq, conv_k=ck, conv_v=cv, xn=xn_hist)
-        # Shapes the fused step does not take (B > 48, wide D): library GEMMs
+        # Shapes the fused step does not take: library GEMMs
         # around the conv-step and decode kernels.
         xn = self._rmsnorm(x.reshape(B, Dd))
         P = xn @ self.W_qkvab.T

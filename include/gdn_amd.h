@@ -305,10 +305,9 @@ int gdn_decode_out_proj_hip(const float* o, const gdn_bf16_t* W, gdn_bf16_t* y, 
  * in place when S_out == S_in) and gdn_decode_out_proj_hip, so a serving loop
  * pays one host call per step.  q, k, v, a, b ([B, H dk] x2, [B, H dv],
  * [B, H] x2 bf16) and o ([B, H dv] fp32) are caller-owned scratch; y is
- * [B, D] bf16.  B <= 48: the projections run as groups of 16 sequences (one
- * gdn_decode_in_proj_hip and one gdn_decode_out_proj_hip launch per group),
- * the recurrence once for all B; other constraints and errors are those of
- * the three entry points.  48 < B <= 65535: RMSNorm (x_n written to y, which
+ * [B, D] bf16.  B <= 16: gdn_decode_in_proj_hip, the recurrence and
+ * gdn_decode_out_proj_hip, whose constraints and errors apply.
+ * 16 < B <= 65535: RMSNorm (x_n written to y, which
  * is then scratch until the out-projection overwrites it, and the x_n
  * history shifted), a tiled in-projection with the conv step in its
  * epilogue, the recurrence, a tiled out-projection; D % 64 == 0, D <= 16384,

@@ -84,10 +84,9 @@ def test_layer_decode_matches_prefill(dev, inplace):
 
 @pytest.mark.parametrize("B", [20, 40, 72, 130])
 def test_layer_decode_above_16_sequences_matches_prefill(dev, B):
-    """17..48 sequences run the fused step as groups of 16 (B=20: a partial
-    second group; B=40: three groups), more the tiled step (B=72: a partial
-    second row tile; B=130: three row tiles, the last with 2 rows); both must
-    agree with one prefill."""
+    """More than 16 sequences run the tiled step (B=20, 40: one partial row
+    tile; B=72: a partial second row tile; B=130: three row tiles, the last
+    with 2 rows); it must agree with one prefill."""
     _, w = _weights(dev, seed=9)
     layer = GDNLayerCustom(w)
     assert layer.fused_decode and layer.tiled_decode
@@ -251,8 +250,8 @@ def test_layer_config5_decode_matches_oracle(dev, B):
     GPU layer and the oracle layer's decode (fp32 projection); four steps on
     each, compared step by step (outputs to the scaled 2e-2 bar), then the
     recurrent state (1e-2 relative), conv caches and x_n history.  B=4 runs
-    the fused decode step, B=20 the fused step as two groups, B=72 and B=130
-    the tiled step (two and three row tiles)."""
+    the skinny fused step, B=20, 72 and 130 the tiled step (one, two and
+    three row tiles)."""
     g, w_cpu, w = _cfg5_weights(dev, seed=12)
     layer, base = GDNLayerCustom(w), GDNLayerBaseline(w_cpu, fp32_proj=True)
     x = torch.randn(B, 196, 2048, generator=g).bfloat16()
