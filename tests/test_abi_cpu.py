@@ -142,7 +142,7 @@ def test_decode_step_validation_errors():
     step_args = lambda B, D, dv: ([FAKE, FAKE, 1e-6] + [FAKE] * 10 + [0.1] + [FAKE] * 8 + [B, D, 2, 128, dv, 4, None])
     with pytest.raises(GdnError, match="decode_step: B=65536, at most 65535"):
         abi.call("gdn_layer_decode_step_hip", *step_args(65536, 2048, 128))
-    # B > 48: the tiled path's own checks
+    # B > 16: the tiled path's own checks
     with pytest.raises(GdnError, match="decode_step: D=100 must be a multiple of 64"):
         abi.call("gdn_layer_decode_step_hip", *step_args(65, 100, 128))
     with pytest.raises(GdnError, match="decode_step: H dk=256 and H dv=32 must be multiples of 64"):
