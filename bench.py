@@ -17,6 +17,9 @@ same-run parity of the GPU results against that oracle:
   events around per-phase launches on the stream the kernels run on.
 * ``prefill_cfg2``: config 2, B=1, T=2048, H=16.
 * ``prefill_batches``: the metric prefill at B=4 and B=8 (timing only).
+* ``prefill_sweep``: the reference's prefill sweep (bench/bench_prefill.py:
+  67-104), B in {1, 8, 32, 64} x T in {2048, 4096, 8192} at H=16,
+  dk=dv=128 (timing only, inputs drawn on the GPU).
 * ``prefill_varlen``: config 4, 8 packed sequences, lengths U[512, 8192]
   (seed 3), nonzero initial states.
 * ``decode``: config 3, B=256, H=32, dk=dv=128, one 512 MiB fp32 state
@@ -31,7 +34,7 @@ same-run parity of the GPU results against that oracle:
   per B, parity against the oracle layer at B=256.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--no-extra] [--only prefill,cfg2,batches,varlen,decode,layer,packed,serve]
+                    [--no-extra] [--only prefill,cfg2,batches,sweep,varlen,decode,layer,packed,serve]
 """
 
 import argparse
@@ -61,7 +64,7 @@ def decode_bytes(B, H):
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-LEGS = ("prefill", "cfg2", "batches", "varlen", "decode", "layer", "packed", "serve")
+LEGS = ("prefill", "cfg2", "batches", "sweep", "varlen", "decode", "layer", "packed", "serve")
 
 
 def measured_traffic(kernel):
@@ -410,6 +413,28 @@ def main():
             log(f"prefill B={Bx} T={T} H={H}: {msx:.4f} ms/step, {Bx * T / (msx / 1e3):.4g} tok/s")
             del gx
         result["prefill_batches"] = batches
+
+    # ----------------------- the reference's prefill sweep, B x T, timing only
+    if "sweep" in legs:
+        # bench/bench_prefill.py:67-104 (and bench_gdn.py:315-329): B in
+        # {1, 8, 32, 64} x T in {2048, 4096, 8192}, here at the metric's
+        # H=16, dk=dv=128 with zero initial state; inputs drawn on the GPU.
+        sweep = {}
+        for Bx in (1, 8, 32, 64):
+            for Tx in (2048, 4096, 8192):
+                gx = synth.prefill_inputs_on_device(Bx, Tx, H, K, V, seed=5, device=dev)
+                for _ in range(2):
+                    prefill_call(gx)
+                msx = time_events(lambda: prefill_call(gx), max(3, min(args.steps, 10)), torch)
+                sweep[f"B{Bx}_T{Tx}"] = {"ms": msx, "tokens_per_s": Bx * Tx / (msx / 1e3),
+                                         **roofline_fracs(PREFILL_FLOP_PER_TOKEN_HEAD * Bx * Tx * H,
+                                                          prefill_bytes(Bx * Tx, H, Bx), msx)}
+                log(f"prefill sweep B={Bx} T={Tx}: {msx:.4f} ms, {Bx * Tx / (msx / 1e3):.4g} tok/s, "
+                    f"{100 * sweep[f'B{Bx}_T{Tx}']['mfma_frac']:.1f}% MFMA")
+                del gx
+        sweep["config"] = ("reference sweep bench/bench_prefill.py:67-104 at H=16, dk=dv=128, zero state; "
+                           "q,k unit rows, v,a,b N(0,1) bf16, drawn on the GPU (seed 5)")
+        result["prefill_sweep"] = sweep
 
     # ------------------------------------- packed variable-length prefill (config 4)
     if "varlen" in legs:

@@ -46,6 +46,27 @@ def prefill_inputs(B, T, H, K=128, V=128, seed=1, state=False, device="cpu"):
     return {key: (val.to(device) if torch.is_tensor(val) else val) for key, val in d.items()}
 
 
+def prefill_inputs_on_device(B, T, H, K=128, V=128, seed=1, device="cuda"):
+    """prefill_inputs' distributions drawn on the device (a generator there):
+    for sizes whose fp32 CPU draws would take gigabytes of host memory.  The
+    values differ from prefill_inputs' at the same seed."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def unit_rows(shape):
+        x = torch.randn(shape, generator=g, device=device)
+        x /= x.norm(dim=-1, keepdim=True)
+        return x.to(torch.bfloat16)
+
+    q = unit_rows((B, H, T, K))
+    k = unit_rows((B, H, T, K))
+    bf = dict(generator=g, device=device)
+    return dict(q=q, k=k, v=torch.randn(B, H, T, V, **bf).to(torch.bfloat16),
+                a=torch.randn(B, H, T, **bf).to(torch.bfloat16), b_logits=torch.randn(B, H, T, **bf).to(torch.bfloat16),
+                A_log=torch.full((H,), LN_HALF, dtype=torch.float32, device=device), dt_bias=0.0,
+                mask=torch.ones(B, T, dtype=torch.float32, device=device), state_in=None)
+
+
 def decode_inputs(B, H, K=128, V=128, seed=0, state=True, device="cpu"):
     """Inputs of the decode kernel contract (q, k [B,H,K]; v [B,H,V]; a, b [B,H])."""
     g = _gen(seed)
