@@ -5,7 +5,8 @@
 //   y = bf16((x * rsqrt(mean(x^2) + eps)) * gamma), all in fp32.
 // Here one wave64 owns a row; each lane moves 16-byte chunks (8 bf16), the
 // row stays in VGPRs between the sum of squares and the scaling, so x is read
-// once and y written once.  Four rows per 256-thread workgroup.
+// once and y written once.  One row per 64-thread workgroup up to 1024 rows,
+// else four rows per 256-thread workgroup.
 //
 // The decode step's launch (gdn_host::rmsnorm_launch with a history) also
 // moves the row's x_n history [R, nc, D] one token older and appends y: each
@@ -23,7 +24,7 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __rest
                                                           uint16_t* __restrict__ y, int R, int D, float eps,
                                                           uint16_t* __restrict__ hist, int nc) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= R) return;
     const int nch = D >> 3;
     const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * D);
@@ -87,7 +88,10 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_kernel(const uint16_t* __rest
 int gdn_host::rmsnorm_launch(const void* x, const void* gamma, void* y, void* hist, int nc, int R, int D, float eps,
                              hipStream_t s) {
     if (nc < 0 || nc > 3) return gdn_host::fail(GDN_ERR_UNSUPPORTED, "rmsnorm: history of %d tokens, at most 3", nc);
-    const dim3 grid((R + 3) / 4), block(256);
+    // Up to a few hundred rows (a decode step's batch), one row per
+    // workgroup spreads them over more CUs; else four rows a workgroup.
+    const int rows_per_wg = R <= 1024 ? 1 : 4;
+    const dim3 grid((R + rows_per_wg - 1) / rows_per_wg), block(64 * rows_per_wg);
     const auto* xp = static_cast<const uint16_t*>(x);
     const auto* gp = static_cast<const uint16_t*>(gamma);
     auto* yp = static_cast<uint16_t*>(y);
