@@ -1137,11 +1137,12 @@ __global__ __launch_bounds__(64 * NW) void gdn_prefill_state_kernel(PrefillParam
 // In the output pass three copy waves do all global memory traffic of the
 // chunk loop: waves 4 and 5 stage chunk c + 1 (half of the copies each)
 // while the compute waves work on chunk c, and wave 6 writes chunk c - 1's
-// outputs, which the compute waves left in LDS, as whole 256-byte rows.  The
-// pass is bound by memory traffic (77 KiB a chunk step): one wave keeps at
-// most ~63 copies in flight, so its rate is capped by memory latency; loads
-// and stores from separate waves flow at the same time; and no compute wave
-// stalls on a full memory queue.  The output pass runs one workgroup per CU
+// outputs, which the compute waves left in LDS, as whole 256-byte rows
+// (77 KiB of memory traffic a chunk step): loads and stores from separate
+// waves flow at the same time, and no compute wave stalls on a full memory
+// queue.  (Staging chunk c + 2 through the loaders' registers, for two steps
+// of copy latency instead of one, measured slower: the step is bound by its
+// LDS traffic, not by the copies' latency.)  The output pass runs one workgroup per CU
 // (one compute wave per SIMD), the map pass two.
 // Per chunk, DMA-staged into one of two LDS buffers:
 //   K   16 fragments, lane slots swizzled (kslot) for the K^T transposing reads
