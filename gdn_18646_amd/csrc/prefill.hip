@@ -1798,10 +1798,20 @@ __global__ __launch_bounds__(512) void gdn_prefill_scan_kernel(PrefillParams p, 
         *reinterpret_cast<lds_u32x2*>(buf + (2 * (wave >> 1)) * kFragB + 16 * lane + half) = hi;
         *reinterpret_cast<lds_u32x2*>(buf + (2 * (wave >> 1) + 1) * kFragB + 16 * lane + half) = pack4_lo(S, hi);
     };
-    publish(sbuf);
+    // From a zero initial state the first step is S_in(1) = psi_0 (phi_0 0 +
+    // psi_0 adds exact zeros), which psi_0's slot already holds: it is taken
+    // as is, one dependent step shorter.
+    const bool zero_start = p.state_in == nullptr;
+    if (!zero_start) publish(sbuf);
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
         if (PLANNED && j >= nsteps) continue;  // uniform over the workgroup (the loop still unrolls)
+        if (j == 0 && zero_start) {
+            S = ps[0];
+            if (D < STEPS && (!PLANNED || D < nsteps)) load(D);
+            publish(sbuf + 8 * kFragB);
+            continue;
+        }
         lds_u8* const buf = sbuf + (j & 1) * 8 * kFragB;
         lds_barrier();
         f32x4 acc_h = ps[j % D];
