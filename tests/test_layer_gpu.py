@@ -100,6 +100,25 @@ def test_layer_decode_above_16_sequences_matches_prefill(dev, B):
     assert_out_close(torch.cat(ys, 1), y_pre, what=f"decode (B={B}) vs prefill")
 
 
+def test_layer_decode_tiled_dv256_matches_prefill(dev):
+    """The tiled step with dv=256 value heads (the reference kernel's own
+    V_DIM: an out-projection K of H dv = 512, eight K slices, and v tiles of
+    256-wide heads) against one prefill."""
+    _, w = _weights(dev, D=256, H=2, DK=128, DV=256, seed=15)
+    layer = GDNLayerCustom(w)
+    assert layer.tiled_decode
+    B = 40
+    x = torch.randn(B, 20, 256, generator=torch.Generator().manual_seed(16)).bfloat16().to(dev)
+    y_all, st_all = layer.forward(x, return_state=True)
+    _, st = layer.forward(x[:, :14], return_state=True)
+    ys = []
+    for t in range(14, 20):
+        y_t, st = layer.decode(x[:, t:t + 1], st, inplace=True)
+        ys.append(y_t)
+    assert_out_close(torch.cat(ys, 1), y_all[:, 14:], what="dv=256 tiled decode vs prefill")
+    assert_state_close(st["recurrent"].cpu(), st_all["recurrent"].cpu())
+
+
 def test_layer_decode_unfused_path_matches_prefill(dev):
     """The unfused step (RMSNorm, library GEMM, conv-step kernel, library GEMM),
     which shapes outside the fused kernels take, against one prefill."""
