@@ -1248,16 +1248,34 @@ __device__ __forceinline__ void stage4_issue(const PrefillParams& p, lds_u8* buf
     }
 }
 
-// The output pass's Aq wave forms the six nonzero fragments of the staged
+// The output pass's copy waves form the six nonzero fragments of the staged
 // chunk's causal Aq = (m scale) (Q K^T o Gamma) into the buffer's Aq area,
-// from the staged Q and K and the token block.  Each 16x16 tile (t, s) is
-// formed transposed, as K_s Q_t^T: its accumulator (lane (n, g): s rows
-// 4 g + i of token column n) is then, packed, half of a fragment (mt, S) as
-// the B operand of dV^T Aq^T reads it (lane (n, g): token 16 mt + n, s in
-// pi order).  Rows past a sequence's end are clamped copies; their tokens
-// have m scale = 0.
+// from the staged Q and K and the token block, each wave the fragments of
+// SLOTS (bit i: fragment i), so that the Aq products are spread over the four
+// SIMDs instead of queueing behind one compute wave's products on one.
+// Each 16x16 tile (t, s) is formed transposed, as K_s Q_t^T: its accumulator
+// (lane (n, g): s rows 4 g + i of token column n) is then, packed, half of a
+// fragment (mt, S) as the B operand of dV^T Aq^T reads it (lane (n, g): token
+// 16 mt + n, s in pi order).  Rows past a sequence's end are clamped copies;
+// their tokens have m scale = 0.
+//   fragment: 0      1            2            3      4            5
+//   tiles:    (0,0)  (1,0),(1,1)  (2,0),(2,1)  (2,2)  (3,0),(3,1)  (3,2),(3,3)
+template <unsigned SLOTS>
 __device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
     using St = Stage4<kModeOut>;
+    constexpr int t_of[6] = {0, 1, 2, 2, 3, 3};
+    constexpr int s_lo[6] = {0, 0, 0, 2, 0, 2};  // first tile's s (the second's is s + 1)
+    constexpr bool two[6] = {false, true, true, false, true, true};
+    auto needs_q = [](int t) {
+        for (int i = 0; i < 6; ++i)
+            if (((SLOTS >> i) & 1) && t_of[i] == t) return true;
+        return false;
+    };
+    auto needs_k = [](int s) {
+        for (int i = 0; i < 6; ++i)
+            if (((SLOTS >> i) & 1) && (s_lo[i] == s || (two[i] && s_lo[i] + 1 == s))) return true;
+        return false;
+    };
     const int n = lane & 15, g = lane >> 4;
     const lds_f32* Hb = reinterpret_cast<const lds_f32*>(buf + St::offH);
     bf16x8 qf[4][4], kf[4][4];
@@ -1265,14 +1283,17 @@ __device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
     f32x4 ls[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+        if (needs_q(t)) {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            qf[t][kk] = frag(buf, St::offQ + (4 * t + kk) * kFragB, lane);
-            kf[t][kk] = kfrag(buf + St::offK, 4 * t + kk, lane);
+            for (int kk = 0; kk < 4; ++kk) qf[t][kk] = frag(buf, St::offQ + (4 * t + kk) * kFragB, lane);
+            lt[t] = Hb[16 * t + n];
+            mt[t] = Hb[64 + 16 * t + n];
         }
-        lt[t] = Hb[16 * t + n];
-        mt[t] = Hb[64 + 16 * t + n];
-        ls[t] = *reinterpret_cast<const lds_f32x4*>(Hb + 16 * t + 4 * g);
+        if (needs_k(t)) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) kf[t][kk] = kfrag(buf + St::offK, 4 * t + kk, lane);
+            ls[t] = *reinterpret_cast<const lds_f32x4*>(Hb + 16 * t + 4 * g);
+        }
     }
     auto tile = [&](int ti, int si) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1287,15 +1308,14 @@ __device__ __forceinline__ void stage4_aq(lds_u8* buf, int lane) {
         return pack4_bf16(v);
     };
     const u32x2 z = {0u, 0u};
-    auto put = [&](int slot, const u32x2 lo, const u32x2 hi) {
-        *reinterpret_cast<lds_u32x4*>(buf + St::offAq + slot * kFragB + 16 * lane) = u32x4{lo[0], lo[1], hi[0], hi[1]};
-    };
-    put(0, tile(0, 0), z);
-    put(1, tile(1, 0), tile(1, 1));
-    put(2, tile(2, 0), tile(2, 1));
-    put(3, tile(2, 2), z);
-    put(4, tile(3, 0), tile(3, 1));
-    put(5, tile(3, 2), tile(3, 3));
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        if ((SLOTS >> i) & 1) {
+            const u32x2 lo = tile(t_of[i], s_lo[i]);
+            const u32x2 hi = two[i] ? tile(t_of[i], s_lo[i] + 1) : z;
+            *reinterpret_cast<lds_u32x4*>(buf + St::offAq + i * kFragB + 16 * lane) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+    }
 }
 
 // The copy wave: chunk c's output tile from LDS to `ob` (row 0, the
@@ -1455,7 +1475,7 @@ __device__ __forceinline__ void state4_step(const lds_u8* buf, f32x4 (&S)[8][NT]
         if (half == 0) {
             load_kt(4);
         } else if constexpr (OUT) {
-            mid();  // the Aq wave has formed Aq
+            mid();  // the copy waves have formed Aq
 #pragma unroll
             for (int i = 0; i < 6; ++i) af[i] = frag(buf, St::offAq + i * kFragB, lane);
 #pragma unroll
@@ -1541,8 +1561,8 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NT>::nWaves)) __attribute__((amd
     const SeqInfo sq = seq_info(p, sidx);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Copy waves (output pass): 4 and 5 copy chunk c + 1 in, 6 writes chunk
-    // c - 1's outputs, 7 forms chunk c's Aq.  In the map pass the compute
-    // waves copy (`issuer`).
+    // c - 1's outputs, and all four form chunk c's Aq.  In the map pass the
+    // compute waves copy (`issuer`).
     const bool loader = OUT && wave >= 4 && wave < 4 + St::loaders;
     const bool storer = OUT && wave == 4 + St::loaders;
     const bool aqw = OUT && wave == 5 + St::loaders;
@@ -1590,7 +1610,7 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NT>::nWaves)) __attribute__((amd
     // k opens step k: chunk c is staged, nobody reads buffer (k + 1) % 2 any
     // more, and chunk c - 1's outputs are in tile (k - 1) % 2.  In the output
     // pass a second barrier per step, in the middle of the compute waves'
-    // state update, publishes chunk c's Aq, formed meanwhile by the Aq wave.
+    // state update, publishes chunk c's Aq, formed meanwhile by the copy waves.
     // The copy waves run their own loop (with the same barriers), so the
     // compute waves' state is not live in it.
     if constexpr (OUT) {
@@ -1601,7 +1621,12 @@ __global__ __launch_bounds__((64 * Stage4<MODE, NT>::nWaves)) __attribute__((amd
                 if (loader) wait_vm<0>();  // chunk c staged
                 lds_barrier();
                 if (loader && c + 1 < c_end) issue(c + 1, (k + 1) & 1);
-                if (aqw) stage4_aq(buf(k & 1), lane);
+                // Chunk c's Aq: each copy wave (one a SIMD) forms 2 or 3 of its 10 tiles.
+                static_assert(St::loaders == 2, "copy waves 4..7");
+                if (wave == 4) stage4_aq<0x28>(buf(k & 1), lane);  // (2,2), (3,2), (3,3)
+                if (wave == 5) stage4_aq<0x11>(buf(k & 1), lane);  // (0,0), (3,0), (3,1)
+                if (wave == 6) stage4_aq<0x04>(buf(k & 1), lane);  // (2,0), (2,1)
+                if (wave == 7) stage4_aq<0x02>(buf(k & 1), lane);  // (1,0), (1,1)
                 // Chunk c - 1 is never a sequence's partial last chunk here.
                 if (storer && k >= 1) stage4_store<true, 2 * St::cols>(obuf((k - 1) & 1), obase(c - 1), orow, kC, lane);
                 lds_barrier();  // chunk c's Aq formed
