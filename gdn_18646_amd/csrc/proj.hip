@@ -18,9 +18,9 @@
 // XOR swizzle that keeps the MFMA fragment reads at linear-read speed.
 // Waves form a 4 x 2 grid of 64 columns x 128 tokens = 4 x 8 MFMA 16x16x32
 // tiles.  In the transposed C layout a lane holds 4 adjacent columns of one
-// token and the 16 tokens of a tile form one DPP row: the conv taps are row
-// shifts.  The bf16 results go into an output tile in LDS (the two stages)
-// and leave as whole rows, 16 bytes per lane.
+// token, 16 tokens a tile: the conv taps are reads of a per-wave LDS window
+// shifted by whole tokens.  The bf16 results go into an output tile in LDS
+// (the two stages) and leave as whole rows, 16 bytes per lane.
 //
 // gdn_proj_conv_kernel (general shapes: group boundaries not on 4 columns,
 // unaligned outputs, K not a multiple of 64) computes 128 x 128 tiles of P whose rows are
@@ -206,21 +206,18 @@ static_assert((kMCols + kMToks) % (8 * kMWaves) == 0 && kMCols % (8 * kMWaves) =
 static_assert(kMToks == 2 * 16 * kWNT, "two token waves");
 constexpr int kMHandB = (kMCols / (16 * kWMT)) * kWMT * 1024;  // hand-over area: one 16-token fp32 tile per column wave and MFMA tile
 static_assert(kMStages * kMStageB == kMToks * kMCols * 2, "the stages hold the bf16 output tile");
+// Conv window per wave: for each column quad a strip of 32 16-byte slots
+// (slots 0..2: the previous 16-token tile's last 3 tokens, 3..18: the current
+// tile's tokens, fp32 x 4 columns), so a tap is a plain b128 read shifted by
+// whole slots, conflict free like a linear read.
+constexpr int kMConvB = kMWaves * 4 * 32 * 16;
+static_assert(kMStages * kMStageB + kMHandB + kMConvB <= 160 * 1024, "LDS");
 
 // Staged row r holds its 8 16-byte chunks (k 8c .. 8c+7) at slot c ^ (r & 7):
 // a fragment read (16 rows, one chunk each) then spreads every 8 consecutive
 // rows over the 8 slots of a 128-byte line, which reads at the rate of a
 // linear ds_read_b128 on gfx950 (measured; (r ^ (r >> 3)) & 7 lost a third).
 __device__ __forceinline__ int swz(int r) { return r & 7; }
-
-// Token n - K of a 16-token tile held one token per lane of a DPP row:
-// row_shr:K inside the tile; lanes n < K take token 16 + n - K of the
-// previous tile (row_ror:K of prev).
-template <int K>
-__device__ __forceinline__ float tap_prev(float cur, float prev) {
-    const int rot = __builtin_amdgcn_mov_dpp(__float_as_int(prev), 0x120 + K, 0xf, 0xf, true);  // every lane valid
-    return __int_as_float(__builtin_amdgcn_update_dpp(rot, __float_as_int(cur), 0x110 + K, 0xf, 0xf, false));
-}
 
 // Packed row table of the launch (ProjParams::row_off), read from the
 // kernel's argument block (the ProjParams argument sits at its start):
@@ -257,7 +254,7 @@ __device__ __forceinline__ gdn_proj::ProjGroup select_group(const gdn_proj::Proj
 template <bool PACKED>
 __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kMWaves / 4, kMWaves / 4))) void gdn_proj_conv_mfma_kernel(
     gdn_proj::ProjParams p, int n_tok, int n_col) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[kMStages * kMStageB + kMHandB];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[kMStages * kMStageB + kMHandB + kMConvB];
     lds_u8* const smem = (lds_u8*)&smem_raw[0];
 
     // Workgroup -> tile.  Dispatch deals workgroups to the 8 XCDs round-robin;
@@ -480,7 +477,7 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
 
     static_for<0, kWMT>([&](auto MT) {
         constexpr int mt = decltype(MT)::value;
-        const int cb = c0 + 16 * kWMT * wm + 16 * mt + 4 * g4;  // this lane's 4 columns (same for the whole DPP row)
+        const int cb = c0 + 16 * kWMT * wm + 16 * mt + 4 * g4;  // this lane's 4 columns (same for the tile's 16 tokens)
         if (cb >= p.D_out) return;
         const gdn_proj::ProjGroup gq = select_group(p, cb);
         const int cc = cb - gq.col0, width = gq.width, hd = gq.head_dim;
@@ -527,6 +524,14 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
         };
         f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
         if (wn == 1) pv = cache_row(*reinterpret_cast<const lds_f32x4*>(xs + mt * 1024), bx, t3x);
+        // This lane's conv window strip; the previous tile's last 3 tokens
+        // (lanes 13..15) go to slots 0..2.
+        lds_u8* const cw = smem + kMStages * kMStageB + kMHandB + (wave * 4 + g4) * 512;
+        if (conv && r16 >= 13) *reinterpret_cast<lds_f32x4*>(cw + (r16 - 13) * 16) = pv;
+        // The window is shared by the wave's lanes, which the compiler's
+        // per-lane view does not see: these fences keep its accesses in
+        // program order (the hardware then runs them in order).
+        asm volatile("" ::: "memory");
         // Unstaged groups (head_dim 1..3 or 4-column aligned only) store from
         // registers.  Element index of (b, t, column cc + i): b width T + t
         // tstride + coff[i] (token-major: tstride = width, coff = cc + i;
@@ -583,17 +588,27 @@ __global__ __launch_bounds__(kMWaves * 64) __attribute__((amdgpu_waves_per_eu(kM
             // conv + SiLU (plain groups: the current row)
             float y[4];
             if (conv) {
+                // Taps through the window: tokens n - 1, n - 2, n - 3 are
+                // slots n + 2, n + 1, n (one wave: its LDS accesses run in
+                // order, so the reads see this tile's writes and the slide of
+                // the last 3 tokens to slots 0..2 comes after every read).
+                *reinterpret_cast<lds_f32x4*>(cw + (3 + r16) * 16) = cur;
+                asm volatile("" ::: "memory");
+                const f32x4 t1 = *reinterpret_cast<const lds_f32x4*>(cw + (2 + r16) * 16);
+                const f32x4 t2 = *reinterpret_cast<const lds_f32x4*>(cw + (1 + r16) * 16);
+                const f32x4 t3v = *reinterpret_cast<const lds_f32x4*>(cw + r16 * 16);
+                asm volatile("" ::: "memory");
+                if (r16 >= 13) *reinterpret_cast<lds_f32x4*>(cw + (r16 - 13) * 16) = cur;
+                asm volatile("" ::: "memory");
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float s = w[i][3] * cur[i] + w[i][2] * tap_prev<1>(cur[i], pv[i]) +
-                                    w[i][1] * tap_prev<2>(cur[i], pv[i]) + w[i][0] * tap_prev<3>(cur[i], pv[i]);
+                    const float s = w[i][3] * cur[i] + w[i][2] * t1[i] + w[i][1] * t2[i] + w[i][0] * t3v[i];
                     y[i] = silu_f(s);
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) y[i] = cur[i];
             }
-            pv = cur;
             if (staged) {
                 *reinterpret_cast<lds_u32x2*>(otile + ounit(nloc, unit) + 8 * g4) =
                     u32x2{pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3])};
