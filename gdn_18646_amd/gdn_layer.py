@@ -187,9 +187,16 @@ class GDNLayerCustom:
         y = o.reshape(B, T, Hh * dv) @ self.W_o.T
         if not return_state:
             return y
+        # x_n history: the last nc normalised tokens, the given state's (zeros
+        # without one) in front when T < nc.  Only those rows are copied.
         nc = self.CK - 1
-        h = torch.cat([st.get('xn', torch.zeros(B, nc, Dd, dtype=x.dtype, device=x.device)), xn], 1)
-        xn_hist = h[:, h.shape[1] - nc:]  # the last nc tokens ([:, -nc:] would keep all of them for nc = 0)
+        if T >= nc:
+            xn_hist = xn[:, T - nc:]
+        else:
+            prev = st.get('xn')
+            if prev is None:
+                prev = torch.zeros(B, nc, Dd, dtype=x.dtype, device=x.device)
+            xn_hist = torch.cat([prev[:, T:], xn], 1)
         return y, dict(recurrent=S, conv_q=outs[5], conv_k=outs[6], conv_v=outs[7], xn=xn_hist.contiguous())
 
     def _forward_packed(self, x, cu_seqlens, mask, return_state, state):
@@ -216,19 +223,30 @@ class GDNLayerCustom:
             return y
         # x_n history: the last K - 1 tokens of each sequence, earlier ones from
         # the given state (zeros without one) where the sequence is shorter.
+        # Only the wanted rows are gathered: from x_n, or from the given state
+        # (zeros without one) for the positions before a sequence's start.
         nc = self.CK - 1
-        prev = st.get('xn')
-        if prev is None:
-            prev = torch.zeros(N, nc, Dd, dtype=xn.dtype, device=x.device)
-        pool = torch.cat([prev.reshape(N * nc, Dd), xn], 0)
-        idx = []
+        from_x, from_prev = ([], []), ([], [])  # (history row, source row)
         for i in range(N):
             lo, hi = int(cu[i]), int(cu[i + 1])
             for j in range(nc):
                 t = hi - nc + j  # packed token index wanted
-                idx.append(N * nc + t if t >= lo else i * nc + nc - (lo - t))
-        hist = pool.index_select(0, torch.tensor(idx, dtype=torch.long, device=x.device)) if idx else \
-            pool.new_zeros(0, Dd)
+                dst = from_x if t >= lo else from_prev
+                dst[0].append(i * nc + j)
+                dst[1].append(t if t >= lo else i * nc + nc - (lo - t))
+        dev = x.device
+        hist = torch.empty(N * nc, Dd, dtype=xn.dtype, device=dev)
+        if from_x[0]:
+            rows = torch.tensor(from_x[0], dtype=torch.long, device=dev)
+            hist.index_copy_(0, rows, xn.index_select(0, torch.tensor(from_x[1], dtype=torch.long, device=dev)))
+        if from_prev[0]:
+            rows = torch.tensor(from_prev[0], dtype=torch.long, device=dev)
+            prev = st.get('xn')
+            if prev is None:
+                hist.index_fill_(0, rows, 0)
+            else:
+                src = prev.reshape(N * nc, Dd).index_select(0, torch.tensor(from_prev[1], dtype=torch.long, device=dev))
+                hist.index_copy_(0, rows, src)
         return y, dict(recurrent=S, conv_q=outs[5], conv_k=outs[6], conv_v=outs[7], xn=hist.reshape(N, nc, Dd))
 
     @torch.no_grad()
