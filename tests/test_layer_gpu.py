@@ -342,6 +342,36 @@ def test_layer_packed_sequences_config4(dev):
         _scaled_close(y_dec[i:i + 1], y_long, f"sequence {i}: decode after the packed prefill")
 
 
+def test_layer_xn_history_through_short_prefills(dev):
+    """Prefills of 1 and 2 tokens (shorter than the conv history) continuing from
+    a state keep the given x_n history's newest rows in front: after 8 + 1 + 2 + 1
+    tokens the history equals one forward's, row for row; and packed sequences of
+    0..2 tokens without a state start their history from zeros, as a batch
+    forward of each does."""
+    _, w = _weights(dev, seed=21)
+    layer = GDNLayerCustom(w)
+    x = torch.randn(2, 12, 256, generator=torch.Generator().manual_seed(22)).bfloat16().to(dev)
+    _, st_all = layer.forward(x, return_state=True)
+    _, st = layer.forward(x[:, :8], return_state=True)
+    for lo, hi in ((8, 9), (9, 11), (11, 12)):
+        _, st = layer.forward(x[:, lo:hi], return_state=True, state=st)
+    assert torch.equal(st["xn"].cpu(), st_all["xn"].cpu())
+    for key in ("conv_q", "conv_k", "conv_v"):
+        assert_out_close(st[key].cpu(), st_all[key].cpu(), what=key)
+    lengths = [2, 0, 1, 5]
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    xp = torch.randn(1, cu[-1], 256, generator=torch.Generator().manual_seed(23)).bfloat16().to(dev)
+    _, stp = layer.forward(xp, cu_seqlens=torch.tensor(cu), return_state=True)
+    for i, n in enumerate(lengths):
+        if n == 0:
+            assert torch.count_nonzero(stp["xn"][i]) == 0
+            continue
+        _, st_i = layer.forward(xp[:, cu[i]:cu[i + 1]], return_state=True)
+        assert torch.equal(stp["xn"][i:i + 1].cpu(), st_i["xn"].cpu()), i
+
+
 def test_layer_packed_edge_lengths_with_state(dev):
     """Empty, 1- and 2-token sequences (shorter than the conv history), a mask and a
     carried-in state (recurrent state, conv caches, x_n history): every sequence of the
