@@ -57,10 +57,10 @@ def recurrence(q, k, v, g, beta, mask, state_in=None, scale=None):
 
 
 def decode_closed_form(q, k, v, S, g, beta, scale):
-    """One decode step in the BASELINE form S_T <- g S_T (I - beta k k^T) + beta v k^T.
+    """One decode step in the closed form S_T <- g S_T (I - beta k k^T) + beta v k^T.
 
-    Works on the transposed state S_T = S^T ([.., V, K]), the convention of the
-    project's brief, and returns (o, S) back in the K-first layout.  Inputs are
+    Works on the transposed state S_T = S^T ([.., V, K]), the value-first
+    convention of that formula, and returns (o, S) back in the K-first layout.  Inputs are
     [B, H, *] float64 arrays, g/beta [B, H].
     """
     q, k, v, S = (np.asarray(x, np.float64) for x in (q, k, v, S))
