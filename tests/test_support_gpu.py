@@ -38,6 +38,24 @@ def test_rmsnorm_reference_shapes(exts, dev, B, T):
     assert diff.max().item() < 5e-2 and (diff / (y32.abs() + 1e-8)).max().item() < 0.02
 
 
+@pytest.mark.parametrize("B,T", [(8, 4096), (32, 2048), (32, 4096)])
+def test_rmsnorm_reference_largest_shapes(exts, dev, B, T):
+    """The reference test's largest shapes (B up to 32, T up to 4096, D=2048,
+    tests/test_rmsnorm.py:63-65), inputs drawn on the GPU; the same
+    float32 formula evaluated by torch on the GPU as the reference: at most one
+    bf16 ulp apart, and the reference test's own bar against nn.RMSNorm."""
+    D = 2048
+    g = torch.Generator(device=dev).manual_seed(B * 13 + T)
+    x = torch.randn(B * T, D, generator=g, device=dev).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).bfloat16()
+    y = exts["rmsnorm"].forward(x, gamma, 1e-6, 256, 2)
+    xf = x.float()
+    y32 = xf * torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + 1e-6) * gamma.float()
+    torch.testing.assert_close(y.float(), y32.bfloat16().float(), rtol=2 ** -7, atol=1e-6)
+    diff = (y.float() - y32).abs()
+    assert diff.max().item() < 5e-2 and (diff / (y32.abs() + 1e-8)).max().item() < 0.02
+
+
 @pytest.mark.parametrize("D", [8, 64, 1000 - 1000 % 8, 4096, 16384])
 def test_rmsnorm_generic_D(exts, dev, D):
     g = torch.Generator().manual_seed(D)
