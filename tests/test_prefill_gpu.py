@@ -187,6 +187,45 @@ def test_prefill_half_width_output_pass(exts, dev, B, H, T, dv, masked):
     assert_state_close(S, S_ref)
 
 
+@pytest.mark.parametrize("B,H,T,masked", [(12, 16, 300, True), (32, 16, 200, False)])
+def test_prefill_full_width_one_group(exts, dev, B, H, T, masked):
+    """More than 128 (sequence, head) pairs: one chunk group and the full-width
+    output pass (128 columns a workgroup), the plan of the reference sweep's
+    B=32 and B=64 points.  Nonzero initial states, a ragged last chunk and
+    masked tokens."""
+    d = synth.prefill_inputs(B, T, H, 128, 128, seed=B + T, state=True)
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(T)
+        mask = (torch.rand(B, T, generator=g) > 0.1).float()
+    out, S = _kernel(exts, d, dev, mask=mask, state_in=d["state_in"])
+    o_ref, S_ref = _oracle(d, mask=mask, state_in=d["state_in"])
+    assert_out_close(out, o_ref)
+    assert_state_close(S, S_ref)
+
+
+def test_prefill_sweep_scale_batch_consistency(exts, dev):
+    """At the reference sweep's scale (B=32, T=2048, H=16: one chunk group,
+    full-width output pass, 512 heads) every sequence must match the same
+    sequence run alone (B=1: eight chunk groups joined through their affine
+    maps, a different plan): sequences 0, 17 and 31 are checked, to the
+    output and state bars of the oracle tests (the oracle itself would take
+    minutes at this size)."""
+    d = synth.prefill_inputs_on_device(32, 2048, 16, 128, 128, seed=77, device=dev)
+    empty = torch.empty(0, device=dev, dtype=torch.float32)
+
+    def run(sl):
+        return exts["prefill"].prefill(d["q"][sl], d["k"][sl], d["v"][sl], d["A_log"], d["a"][sl], 0.0,
+                                       d["b_logits"][sl], d["mask"][sl], empty, 0.0)
+
+    out, S = run(slice(0, 32))
+    for b in (0, 17, 31):
+        o1, S1 = run(slice(b, b + 1))
+        torch.cuda.synchronize()
+        assert_out_close(out[b:b + 1].cpu(), o1.cpu(), what=f"sequence {b}")
+        assert_state_close(S[b:b + 1].cpu(), S1.cpu(), what=f"state {b}")
+
+
 @pytest.mark.parametrize("B,H,T,dv", [(1, 16, 8192, 128), (2, 3, 130, 128), (1, 2, 1500, 64), (3, 5, 100, 48),
                                        (2, 4, 257, 256)])
 def test_prefill_token_major_output(exts, dev, B, H, T, dv):
