@@ -1332,8 +1332,8 @@ __device__ __forceinline__ void stage4_store(const lds_u8* obuf, uint16_t* ob, i
     for (int i = 0; i < kC * LPR / 64; ++i) {
         const int row = (64 / LPR) * i + lane / LPR;
         const u32x4 v = *reinterpret_cast<const lds_u32x4*>(obuf + row * kObPitch + (lane % LPR) * 16);
-        if (FULL || row < nvalid)
-            *reinterpret_cast<u32x4*>(ob + static_cast<size_t>(row) * orow + (lane % LPR) * 8) = v;
+        if (FULL || row < nvalid)  // streamed out: nothing in this pass reads the outputs back
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(ob + static_cast<size_t>(row) * orow + (lane % LPR) * 8));
     }
 }
 
