@@ -204,6 +204,40 @@ def test_prefill_full_width_one_group(exts, dev, B, H, T, masked):
     assert_state_close(S, S_ref)
 
 
+def test_prefill_graph_replays_match_eager(exts, dev):
+    """The prefill (intra kernel, map pass, scan, output pass: 4 chunk groups
+    here) captured in a HIP graph: three replays on new inputs copied into the
+    captured input tensors, with eager work and a synchronisation between them,
+    each bit-identical to an eager call on the same inputs (the path holds no
+    memset node whose replays could go stale)."""
+    B, H, T = 1, 4, 1000
+    ins = [synth.prefill_inputs(B, T, H, 128, 128, seed=40 + i, state=True) for i in range(4)]
+    keys = ("q", "k", "v", "a", "b_logits", "state_in")
+    static = {k: ins[0][k].to(dev).clone() for k in keys}
+    A_log = ins[0]["A_log"].to(dev)
+    mask = ins[0]["mask"].to(dev)
+
+    def call():
+        return exts["prefill"].prefill(static["q"], static["k"], static["v"], A_log, static["a"], 0.0,
+                                       static["b_logits"], mask, static["state_in"], 0.0)
+
+    call()  # warm the allocator and the library outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g, S_g = call()
+    for d in ins[1:]:
+        for k in keys:
+            static[k].copy_(d[k].to(dev))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_o, got_S = out_g.clone(), S_g.clone()
+        ref_o, ref_S = call()  # eager, same inputs
+        torch.cuda.synchronize()
+        assert torch.equal(got_o, ref_o) and torch.equal(got_S, ref_S)
+        _ = torch.randn(1 << 20, device=dev).sum()  # unrelated eager work between replays
+
+
 def test_prefill_sweep_scale_batch_consistency(exts, dev):
     """At the reference sweep's scale (B=32, T=2048, H=16: one chunk group,
     full-width output pass, 512 heads) every sequence must match the same
