@@ -368,14 +368,17 @@ int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
 
 // ---------------------------------------------------------------------------
 // Decode-step projections for larger batches: 64 x 64 output tiles
-// (sequences x weight rows) on MFMA.
+// (sequences x weight rows) on MFMA for the in-projection, 64 x 32 for the
+// out-projection, whose 4x smaller weight matrix would otherwise give a
+// quarter of the workgroups (64 x 32 tiles: 0.4-0.8 us less a decode step at
+// config 5, B = 32..256).
 //
 // The skinny kernel streams the weights once per group of 16 sequences; here
 // the row tiles of one weight tile are dispatched to the same XCD, so the
 // weights cross HBM about once and the row tiles share them through that
 // XCD's L2.  K moves through LDS in 64-wide slices, DMA'd into a ring of
 // stages.  Eight waves: waves 0-3 take the first 32 K of every slice, waves
-// 4-7 the second, each wave a 32 x 32 block of the tile; the two halves'
+// 4-7 the second, each wave a 32 x TN/2 block of the tile; the two halves'
 // sums meet in LDS at the end.  (A workgroup's load rate grows with its wave
 // count -- measured from L2, 4 waves pull ~90 GB/s, 8 waves ~130 -- and the
 // K split keeps LDS reads at one pass over each slice.)  In LDS, tile rows
@@ -394,12 +397,11 @@ int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
 // the reference's o.to(bf16)); y = bf16(o W_o^T).
 // ---------------------------------------------------------------------------
 constexpr int kTlM = 64;    // sequences per tile
-constexpr int kTlN = 64;    // weight rows (output columns) per tile
+constexpr int kTlN = 64;    // weight rows (output columns) per in-projection tile
+constexpr int kTlNOut = 32;  // ... per out-projection tile (twice the workgroups: W_o is a quarter of the weights)
 constexpr int kTlK = 64;    // K per LDS stage
 constexpr int kTlWaves = 8;
 constexpr int kTlThreads = 64 * kTlWaves;
-constexpr int kTlEC = kTlM * kTlN / kTlThreads;  // epilogue columns per thread (8)
-constexpr int kTlPitch = kTlN + 4;  // fp32 words per row of the epilogue's P tile (16-byte rows, no conflicts)
 
 struct TileParams {
     const uint16_t* W;       // [N, K]
@@ -415,20 +417,30 @@ struct TileParams {
     int width[5];
 };
 
-template <int MODE>
+// TN weight rows per tile: 64 (in-projection) or 32 (out-projection).
+template <int MODE, int TN>
 struct TileCfg {
     static constexpr int kABytes = kTlM * kTlK * 2;  // A slice of one stage
-    static constexpr int kBBytes = kTlN * kTlK * 2;
+    static constexpr int kBBytes = TN * kTlK * 2;
     static constexpr int kStageBytes = kABytes + kBBytes;
     static constexpr int kStages = 4;
+    // A W slice of 32 rows is 4 KB: each wave copies 512 bytes with its
+    // lanes 0..31, so every wave still issues one copy per slice and the
+    // vmcnt waits stay the same on all waves.
+    static constexpr int kBLanes = TN >= 64 ? 64 : 32;
     static constexpr int kADma = kABytes / (1024 * kTlWaves);  // 1 KB DMA instructions per wave per stage
-    static constexpr int kBDma = kBBytes / (1024 * kTlWaves);
+    static constexpr int kBDma = kBBytes / (16 * kBLanes * kTlWaves);
     static constexpr int kDma = kADma + kBDma;
     static constexpr int kRingBytes = kStages * kStageBytes;
-    static constexpr int kTapOff = kRingBytes;  // MODE 0: conv taps [kTlN][4] bf16, right-aligned
-    static constexpr int kLdsBytes = kRingBytes + (MODE == 0 ? kTlN * 8 : 0);
-    static_assert(kTlM * kTlPitch * 4 <= kRingBytes, "the epilogue's P tile reuses the ring");
-    static_assert(kADma >= 1 && kBDma >= 1, "every wave issues whole 1 KB blocks");
+    static constexpr int kTapOff = kRingBytes;  // MODE 0: conv taps [TN][4] bf16, right-aligned
+    static constexpr int kLdsBytes = kRingBytes + (MODE == 0 ? TN * 8 : 0);
+    static constexpr int kNI = TN / 32;                     // 16-column fragments per wave
+    static constexpr int kEC = kTlM * TN / kTlThreads;      // epilogue columns per thread (8 or 4)
+    static constexpr int kPitch = TN + 4;                   // fp32 words per row of the epilogue's P tile
+    static_assert(kTlM * kPitch * 4 <= kRingBytes, "the epilogue's P tile reuses the ring");
+    static_assert(kADma >= 1 && kBDma >= 1, "every wave issues whole copies");
+    static_assert(kBBytes % (16 * kBLanes * kTlWaves) == 0 && TN % 32 == 0, "W slice split over the waves");
+    static_assert(kEC * 8 == TN && (MODE == 1 || TN == 64), "epilogue: 8 threads a row; conv tiles are 64 wide");
 };
 
 // Byte offset in a stage of (row r, 16-byte chunk c) of a slice: 8 chunks a
@@ -442,10 +454,11 @@ struct U16Arr { uint16_t v[N]; };
 template <int N>
 struct U4Arr { u32x4 v[N]; };
 
-// NC = conv_k - 1 (MODE 0; 0 for MODE 1).
-template <int MODE, int NC>
+// NC = conv_k - 1 (MODE 0; 0 for MODE 1); TN weight rows per tile.
+template <int MODE, int NC, int TN>
 __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams p) {
-    using Cfg = TileCfg<MODE>;
+    using Cfg = TileCfg<MODE, TN>;
+    constexpr int EC = Cfg::kEC, PITCH = Cfg::kPitch, NI = Cfg::kNI;
     __shared__ __attribute__((aligned(1024))) unsigned char s_tile[Cfg::kLdsBytes];
     lds_u8* const ring = (lds_u8*)&s_tile[0];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -455,7 +468,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     const int id = blockIdx.x, xcd = id & 7, j8 = id >> 3;
     const int mt = j8 % p.mtiles, nt = xcd + 8 * (j8 / p.mtiles);
     if (nt >= p.ntiles) return;
-    const int m0 = mt * kTlM, n0 = nt * kTlN;
+    const int m0 = mt * kTlM, n0 = nt * TN;
     const int nk = p.K / kTlK;
     // K slice order: column tile nt starts at slice nt % nk, so the
     // workgroups are spread over the slices (and the memory channels that
@@ -464,13 +477,13 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     const int kstart = nt % nk;
 
     // Output group of the tile (uniform): q/k/v tiles never straddle groups
-    // (their widths are multiples of kTlN); a and b share the tiles after v.
+    // (their widths are multiples of TN); a and b share the tiles after v.
     const int g = MODE == 0 ? (n0 >= p.col0[3] ? 3 : n0 >= p.col0[2] ? 2 : n0 >= p.col0[1] ? 1 : 0) : 0;
     const bool conv_tile = MODE == 0 && g < 3;
 
     // Epilogue ownership: thread t takes row t / 8 of the tile, columns
-    // 8 (t % 8) .. + 7.
-    const int er = tid >> 3, ec0 = kTlEC * (tid & 7);
+    // EC (t % 8) .. + EC - 1.
+    const int er = tid >> 3, ec0 = EC * (tid & 7);
     const int eb = m0 + er;
     const int eb_ld = min(eb, p.B - 1);
 
@@ -493,7 +506,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
 #pragma unroll
                 for (int u = 0; u < NC; ++u) hold[u] = buffer_load16(crs, voff, 16 * u);
             }
-            if (tid < kTlN) {
+            if (tid < TN) {
                 const uint16_t* wr = p.conv_w + static_cast<size_t>(n0 + tid) * (NC + 1);
 #pragma unroll
                 for (int e = 0; e <= NC; ++e) tap[3 - NC + e] = wr[e];
@@ -507,7 +520,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     uint32_t aoff[Cfg::kADma], boff[Cfg::kBDma];
 #pragma unroll
     for (int u = 0; u < Cfg::kBDma; ++u) {
-        const int r = 8 * (wave + kTlWaves * u) + (lane >> 3);
+        const int r = Cfg::kBLanes / 8 * (wave + kTlWaves * u) + (lane >> 3);
         const int c = (lane & 7) ^ ((r >> 1) & 7);
         boff[u] = static_cast<uint32_t>(min(r, p.N - 1 - n0) * p.K + 8 * c) * 2;
     }
@@ -523,18 +536,21 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
 #pragma unroll
         for (int u = 0; u < Cfg::kADma; ++u) dma16(p.A + k0, aoff[u], st + (wave + kTlWaves * u) * 1024);
 #pragma unroll
-        for (int u = 0; u < Cfg::kBDma; ++u) dma16(Wt + k0, boff[u], st + Cfg::kABytes + (wave + kTlWaves * u) * 1024);
+        for (int u = 0; u < Cfg::kBDma; ++u)
+            if (Cfg::kBLanes == 64 || lane < Cfg::kBLanes)
+                dma16(Wt + k0, boff[u], st + Cfg::kABytes + (wave + kTlWaves * u) * (16 * Cfg::kBLanes));
     };
 
-    // wave = 4 kh + 2 wm + wn: K half kh of every slice, rows 32 wm, columns 32 wn
+    // wave = 4 kh + 2 wm + wn: K half kh of every slice, rows 32 wm, columns
+    // TN / 2 wn (NI 16-column fragments)
     const int kh = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
     const int r16 = lane & 15, g4 = lane >> 4;
     const int kc = 4 * kh + g4;  // the lane's 16-byte chunk of every slice row
-    f32x4 acc[2][2];
+    f32x4 acc[2][NI];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
     // The wave's A and W fragments of the slice in `slot`.
     auto read_frags = [&](int slot, bf16x8* af, bf16x8* bw) {
         const lds_u8* const sa = ring + slot * Cfg::kStageBytes;
@@ -543,8 +559,8 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
         for (int mi = 0; mi < 2; ++mi)
             af[mi] = *reinterpret_cast<const lds_bf16x8*>(sa + tl_off(32 * wm + 16 * mi + r16, kc));
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-            bw[ni] = *reinterpret_cast<const lds_bf16x8*>(sb + tl_off(32 * wn + 16 * ni + r16, kc));
+        for (int ni = 0; ni < NI; ++ni)
+            bw[ni] = *reinterpret_cast<const lds_bf16x8*>(sb + tl_off(TN / 2 * wn + 16 * ni + r16, kc));
     };
 
     // Slices s go to slot s % S.  All S slots fill first; at iteration i
@@ -560,7 +576,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     else
         wait_vm<0>();
     lds_barrier();
-    bf16x8 af[2], bw[2];
+    bf16x8 af[2], bw[NI];
     read_frags(0, af, bw);
     for (int i = 0; i < nk; ++i) {
         // Slice i + 1 has landed when at most the S - 2 slices issued after
@@ -577,29 +593,29 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma16x16x32(af[mi], bw[ni], acc[mi][ni]);
+            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma16x16x32(af[mi], bw[ni], acc[mi][ni]);
         // slice i + 1's fragments (past the last slice: a valid slot, unused)
         read_frags((i + 1) % S, af, bw);
     }
 
-    // P tile [kTlM][kTlPitch] fp32 over the ring (every wave is past its
+    // P tile [kTlM][PITCH] fp32 over the ring (every wave is past its
     // last read of it after the first barrier): the second K half's sums,
     // then the first half's added.
     lds_barrier();
     lds_f32* const ps = (lds_f32*)ring;
     auto ps_at = [&](int mi, int ni, int e) {
-        return (32 * wm + 16 * mi + 4 * g4 + e) * kTlPitch + 32 * wn + 16 * ni + r16;
+        return (32 * wm + 16 * mi + 4 * g4 + e) * PITCH + TN / 2 * wn + 16 * ni + r16;
     };
     if (kh == 1) {
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
+            for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) ps[ps_at(mi, ni, e)] = acc[mi][ni][e];
     }
     if constexpr (MODE == 0) {
-        if (conv_tile && tid < kTlN)
+        if (conv_tile && tid < TN)
             *reinterpret_cast<lds_u32x2*>(ring + Cfg::kTapOff + 8 * tid) =
                 u32x2{static_cast<uint32_t>(tap[0]) | (static_cast<uint32_t>(tap[1]) << 16),
                       static_cast<uint32_t>(tap[2]) | (static_cast<uint32_t>(tap[3]) << 16)};
@@ -609,28 +625,32 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
+            for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) ps[ps_at(mi, ni, e)] = acc[mi][ni][e] + ps[ps_at(mi, ni, e)];
     }
     lds_barrier();
     if (eb >= p.B) return;
-    float P[kTlEC];
+    float P[EC];
 #pragma unroll
-    for (int u = 0; u < kTlEC / 4; ++u) {
-        const f32x4 v = *reinterpret_cast<const lds_f32x4*>(ring + 4 * (er * kTlPitch + ec0 + 4 * u));
+    for (int u = 0; u < EC / 4; ++u) {
+        const f32x4 v = *reinterpret_cast<const lds_f32x4*>(ring + 4 * (er * PITCH + ec0 + 4 * u));
 #pragma unroll
         for (int e = 0; e < 4; ++e) P[4 * u + e] = v[e];
     }
     if constexpr (MODE == 1) {
         if (n0 + ec0 >= p.N) return;
-        *reinterpret_cast<u32x4*>(p.y + static_cast<size_t>(eb) * p.N + n0 + ec0) =
-            u32x4{pack2_bf16(P[0], P[1]), pack2_bf16(P[2], P[3]), pack2_bf16(P[4], P[5]), pack2_bf16(P[6], P[7])};
+        uint16_t* const yo = p.y + static_cast<size_t>(eb) * p.N + n0 + ec0;
+        if constexpr (EC == 8)
+            *reinterpret_cast<u32x4*>(yo) = u32x4{pack2_bf16(P[0], P[1]), pack2_bf16(P[2], P[3]),
+                                                  pack2_bf16(P[4], P[5]), pack2_bf16(P[6], P[7])};
+        else
+            *reinterpret_cast<u32x2*>(yo) = u32x2{pack2_bf16(P[0], P[1]), pack2_bf16(P[2], P[3])};
     } else if (!conv_tile) {
         // a / b columns: per column (the a | b boundary may fall inside the
         // thread's 8).
 #pragma unroll
-        for (int j = 0; j < kTlEC; ++j) {
+        for (int j = 0; j < EC; ++j) {
             const int n = n0 + ec0 + j;
             if (n < p.N) {
                 const int gi = n >= p.col0[4] ? 4 : 3;
@@ -643,25 +663,25 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
         // Conv taps of the 8 columns (4 bf16 each, right-aligned: slot 3
         // multiplies the new token, slots 3 - NC .. 2 the cached tokens,
         // oldest first).
-        U16Arr<4 * kTlEC> tp;
+        U16Arr<4 * EC> tp;
         {
-            U4Arr<kTlEC / 2> t4;
+            U4Arr<EC / 2> t4;
 #pragma unroll
-            for (int u = 0; u < kTlEC / 2; ++u)
+            for (int u = 0; u < EC / 2; ++u)
                 t4.v[u] = *reinterpret_cast<const lds_u32x4*>(ring + Cfg::kTapOff + 8 * ec0 + 16 * u);
-            tp = __builtin_bit_cast(U16Arr<4 * kTlEC>, t4);
+            tp = __builtin_bit_cast(U16Arr<4 * EC>, t4);
         }
-        float yv[kTlEC];
-        U16Arr<(NC > 0 ? kTlEC * NC : 1)> nwc;
-        U16Arr<(NC > 0 ? kTlEC * NC : 1)> old;
+        float yv[EC];
+        U16Arr<(NC > 0 ? EC * NC : 1)> nwc;
+        U16Arr<(NC > 0 ? EC * NC : 1)> old;
         if constexpr (NC > 0) {
             U4Arr<NC> h;
 #pragma unroll
             for (int u = 0; u < NC; ++u) h.v[u] = hold[u];
-            old = __builtin_bit_cast(U16Arr<kTlEC * NC>, h);
+            old = __builtin_bit_cast(U16Arr<EC * NC>, h);
         }
 #pragma unroll
-        for (int j = 0; j < kTlEC; ++j) {
+        for (int j = 0; j < EC; ++j) {
             float s = bf2f(tp.v[4 * j + 3]) * P[j];
 #pragma unroll
             for (int e = 0; e < NC; ++e) s += bf2f(tp.v[4 * j + 3 - NC + e]) * bf2f(old.v[NC * j + e]);
@@ -685,17 +705,18 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
 
 template <int MODE>
 int launch_tile(TileParams& p, hipStream_t st, const char* who) {
+    constexpr int TN = MODE == 1 ? kTlNOut : kTlN;
     p.mtiles = (p.B + kTlM - 1) / kTlM;
-    p.ntiles = (p.N + kTlN - 1) / kTlN;
+    p.ntiles = (p.N + TN - 1) / TN;
     const dim3 grid(p.mtiles * ((p.ntiles + 7) / 8) * 8);
     if constexpr (MODE == 1) {
-        hipLaunchKernelGGL((gdn_decode_tile_kernel<1, 0>), grid, dim3(kTlThreads), 0, st, p);
+        hipLaunchKernelGGL((gdn_decode_tile_kernel<1, 0, TN>), grid, dim3(kTlThreads), 0, st, p);
     } else {
         switch (p.conv_k - 1) {
-            case 0: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 0>), grid, dim3(kTlThreads), 0, st, p); break;
-            case 1: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 1>), grid, dim3(kTlThreads), 0, st, p); break;
-            case 2: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 2>), grid, dim3(kTlThreads), 0, st, p); break;
-            default: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 3>), grid, dim3(kTlThreads), 0, st, p); break;
+            case 0: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 0, TN>), grid, dim3(kTlThreads), 0, st, p); break;
+            case 1: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 1, TN>), grid, dim3(kTlThreads), 0, st, p); break;
+            case 2: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 2, TN>), grid, dim3(kTlThreads), 0, st, p); break;
+            default: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 3, TN>), grid, dim3(kTlThreads), 0, st, p); break;
         }
     }
     return gdn_host::check_launch(who);

@@ -117,8 +117,8 @@ class GDNLayerCustom:
         self.dt_bias_vec = _dt_bias_for_decode(dtb, self.H).float().contiguous()
         self.W_o = w['W_o'].contiguous()
         self.gamma = w['norm_gamma'].contiguous()
-        # Fused decode step: skinny projections for B <= 16, 64 x 64 MFMA
-        # tiles above.
+        # Fused decode step: skinny projections for B <= 16, MFMA tiles
+        # above.
         Hk, Hv = self.H * self.DK, self.H * self.DV
         self.fused_decode = (self.D % 32 == 0 and self.D <= 4096 and Hv % 32 == 0
                              and Hv <= 4096 and 1 <= self.CK <= 4)
