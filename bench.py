@@ -104,6 +104,40 @@ def time_events(fn, iters, torch):
     return s.elapsed_time(e) / iters
 
 
+class DeviceSettle:
+    """Unrelated GPU work run before each timed leg: bf16 8192 x 8192 x 8192
+    GEMMs and 256 MiB copies for ``ms`` milliseconds, so that the device's
+    power management is in its loaded state when the leg's own warm-up
+    starts.  Measured on MI355X after 3 s idle: the B=1, T=8192 prefill's
+    first 100 calls average 88.6 us and the calls after the first ~200 run
+    81.8 us; B=8, T=8192 goes 0.45 -> 0.373 ms over its first ~60 calls; and
+    300 ms of this load before 5 warm-up + 20 timed calls gives the settled
+    figures (80 us, 0.37 ms) where no load gives 87 us and 0.45 ms.  None of
+    it touches a leg's inputs, outputs or kernels."""
+
+    def __init__(self, torch, dev, ms):
+        self.torch, self.ms = torch, ms
+        if ms > 0:
+            self.a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+            self.b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+            self.src = torch.ones(64 << 20, device=dev)
+            self.dst = torch.empty_like(self.src)
+
+    def __call__(self):
+        if self.ms <= 0:
+            return
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < self.ms:
+            for _ in range(4):
+                self.torch.matmul(self.a, self.b)
+                self.dst.copy_(self.src)
+            self.torch.cuda.synchronize()
+
+    def describe(self):
+        return {"ms": self.ms, "load": "bf16 8192^3 GEMMs + 256 MiB copies (unrelated buffers), before each timed "
+                                       "leg's warm-up"}
+
+
 def time_cpu(fn, reps):
     """Seconds per call of fn() after one warm-up call, and the warm-up's result."""
     res = fn()
@@ -134,7 +168,7 @@ def roofline_fracs(flop, nbytes, ms):
     return {"tflops": tf, "mfma_frac": tf / PEAK_BF16_TFLOPS, "gbs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS}
 
 
-def packed_leg(exts, dev, cpu, nthr, torch, args):
+def packed_leg(exts, dev, cpu, nthr, torch, args, settle):
     """GDNLayerCustom.forward(x, cu_seqlens=...) on config 4's 8 packed lengths
     (U[512, 8192], seed 3) at config 5's dims: RMSNorm, one packed in-projection
     launch (+ conv + SiLU, per-sequence conv caches), the packed prefill and the
@@ -155,6 +189,8 @@ def packed_leg(exts, dev, cpu, nthr, torch, args):
     for n in lengths:
         cu.append(cu[-1] + n)
     y = layer.forward(x, cu_seqlens=cu)
+    settle()
+    layer.forward(x, cu_seqlens=cu)
     ms = time_events(lambda: layer.forward(x, cu_seqlens=cu), max(3, args.steps // 4), torch)
     ncols = 2 * LH * 128 + LH * 128 + 2 * LH
     flop = 2 * Tt * LD * ncols + PREFILL_FLOP_PER_TOKEN_HEAD * Tt * LH + 2 * Tt * LH * 128 * LD
@@ -172,7 +208,7 @@ def packed_leg(exts, dev, cpu, nthr, torch, args):
     return leg
 
 
-def serve_leg(exts, dev, cpu, nthr, torch):
+def serve_leg(exts, dev, cpu, nthr, torch, settle):
     """GDNLayerCustom.decode at B in {1, 8, 32, 64, 128, 256}, config-5 dims (the
     reference's layer decode sweep, bench_gdn.py:332-342): one step = RMSNorm,
     q/k/v/a/b projection + conv step, the recurrence (state in place), W_o.
@@ -208,6 +244,7 @@ def serve_leg(exts, dev, cpu, nthr, torch):
         def step():
             layer.decode(xs[next(it) % len(xs)], st, inplace=True)
 
+        settle()
         for _ in range(3):
             step()
         ms = time_events(step, 100 if SB <= 64 else 50, torch)
@@ -259,6 +296,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the metric prefill and the config-3 decode")
     ap.add_argument("--only", default="", help="comma list of legs to run: " + ",".join(LEGS))
+    ap.add_argument("--settle-ms", type=int, default=300,
+                    help="unrelated GPU load (ms) before each timed leg's warm-up; 0 disables")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device copies of exactly 256 MiB (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -297,6 +336,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     H = 16
+    settle = DeviceSettle(torch, dev, args.settle_ms)
     empty = torch.empty(0, device=dev, dtype=torch.float32)
     pf = exts["prefill"]
     result = {}
@@ -320,10 +360,17 @@ def main():
     if "prefill" in legs:
         d = synth.prefill_inputs(B, T, H, K, V, seed=1)
         g = on_dev(d)
+        # the same W + K calls first without the settle load (reported beside the value)
+        for _ in range(args.warmup):
+            prefill_call(g)
+        torch.cuda.synchronize()
+        ms_unsettled = time_events(lambda: prefill_call(g), args.steps, torch)
+        settle()
         for _ in range(args.warmup):
             prefill_call(g)
         torch.cuda.synchronize()
         ms_prefill = time_events(lambda: prefill_call(g), args.steps, torch)
+        result["device_settle"] = {**settle.describe(), "metric_ms_per_step_without": ms_unsettled}
         out_gpu, S_gpu = prefill_call(g)
         torch.cuda.synchronize()
 
@@ -337,7 +384,9 @@ def main():
                 0.0, g["b_logits"].data_ptr(), g["mask"].data_ptr(), None, 0.0, out_ph.data_ptr(), S_ph.data_ptr(),
                 B, H, T, K, V, ws.data_ptr(), ws_bytes, stream)
         abi.call("gdn_prefill_hip", *ptrs)
+        settle()
         ms_intra = time_events(lambda: abi.call("gdn_prefill_intra_hip", *ptrs), args.steps, torch)
+        settle()
         ms_state = time_events(lambda: abi.call("gdn_prefill_state_hip", *ptrs), args.steps, torch)
         del ws, out_ph, S_ph
 
@@ -380,6 +429,7 @@ def main():
     if "cfg2" in legs:
         d2 = synth.prefill_inputs(1, 2048, H, K, V, seed=1)
         g2 = on_dev(d2)
+        settle()
         for _ in range(3):
             prefill_call(g2)
         ms2 = time_events(lambda: prefill_call(g2), args.steps, torch)
@@ -404,6 +454,7 @@ def main():
         batches = {}
         for Bx in (4, 8):
             gx = on_dev(synth.prefill_inputs(Bx, T, H, K, V, seed=1))
+            settle()
             for _ in range(2):
                 prefill_call(gx)
             msx = time_events(lambda: prefill_call(gx), max(3, args.steps // 2), torch)
@@ -423,6 +474,7 @@ def main():
         for Bx in (1, 8, 32, 64):
             for Tx in (2048, 4096, 8192):
                 gx = synth.prefill_inputs_on_device(Bx, Tx, H, K, V, seed=5, device=dev)
+                settle()
                 for _ in range(2):
                     prefill_call(gx)
                 msx = time_events(lambda: prefill_call(gx), max(3, min(args.steps, 10)), torch)
@@ -446,6 +498,7 @@ def main():
             return pf.prefill_varlen(gl_["q"], gl_["k"], gl_["v"], gl_["A_log"], gl_["a"], 0.0, gl_["b_logits"],
                                      dl["cu_seqlens"], gl_["state_in"], 0.0)
 
+        settle()
         for _ in range(2):
             step_vl()
         msv = time_events(step_vl, max(3, args.steps // 2), torch)
@@ -484,6 +537,7 @@ def main():
             dec1.forward(g1["q"], g1["k"], g1["v"], g1["a"], g1["b"], g1["A_log"], g1["dt_bias"], g1["S"], scale1,
                          o1, S1)
 
+        settle()
         for _ in range(5):
             step1()
         ms1 = time_events(step1, 200, torch)
@@ -530,6 +584,7 @@ def main():
             o_chk.append(o_dev.cpu())
         S_chk = S_chk.cpu()
 
+        settle()
         for i in range(max(args.warmup, 1)):
             st = gsteps[i % len(gsteps)]
             dec.forward(st["q"], st["k"], st["v"], st["a"], st["b"], A_log_d, dtb_d, S_dev, scale, o_dev, S_dev)
@@ -597,12 +652,15 @@ def main():
         xl = x_cpu.to(dev)
         xd = [torch.randn(LB, 1, LD, generator=gl).bfloat16().to(dev) for _ in range(8)]
         y_l, st_l = layer.forward(xl, return_state=True)
+        settle()
+        layer.forward(xl)
         ms_lf = time_events(lambda: layer.forward(xl), max(3, args.steps // 4), torch)
         it_l = iter(range(10 ** 9))
 
         def layer_dec():
             layer.decode(xd[next(it_l) % len(xd)], st_l, inplace=True)
 
+        settle()
         for _ in range(3):
             layer_dec()
         ms_ld = time_events(layer_dec, 128, torch)
@@ -647,11 +705,11 @@ def main():
 
     # ------------------------------- packed layer forward (config-4 lengths, config-5 dims)
     if "packed" in legs:
-        result["layer_packed"] = packed_leg(exts, dev, cpu, nthr, torch, args)
+        result["layer_packed"] = packed_leg(exts, dev, cpu, nthr, torch, args, settle)
 
     # ------------------------------- layer decode at serving batch sizes (config-5 dims)
     if "serve" in legs:
-        result["layer_decode_batches"] = serve_leg(exts, dev, cpu, nthr, torch)
+        result["layer_decode_batches"] = serve_leg(exts, dev, cpu, nthr, torch, settle)
 
     line = {
         "metric": "prefill tokens/s (T=8192) + decode steps/s (B=256); % of MFMA / HBM roofline",
