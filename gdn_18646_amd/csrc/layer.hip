@@ -367,11 +367,11 @@ int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode-step projections for larger batches: 64 x 64 output tiles
-// (sequences x weight rows) on MFMA for the in-projection, 64 x 32 for the
-// out-projection, whose 4x smaller weight matrix would otherwise give a
-// quarter of the workgroups (64 x 32 tiles: 0.4-0.8 us less a decode step at
-// config 5, B = 32..256).
+// Decode-step projections for larger batches: output tiles of 64 sequences x
+// 32 or 64 weight rows on MFMA.  The out-projection (a 4x smaller weight
+// matrix) always takes 32-wide tiles, the in-projection while the batch fits
+// one row tile; both give twice the workgroups of 64-wide tiles (1.2-1.6 us
+// less a decode step at config 5, B = 17..64) with bit-identical results.
 //
 // The skinny kernel streams the weights once per group of 16 sequences; here
 // the row tiles of one weight tile are dispatched to the same XCD, so the
@@ -397,7 +397,8 @@ int launch_skinny(SkinnyParams& p, hipStream_t st, const char* who) {
 // the reference's o.to(bf16)); y = bf16(o W_o^T).
 // ---------------------------------------------------------------------------
 constexpr int kTlM = 64;    // sequences per tile
-constexpr int kTlN = 64;    // weight rows (output columns) per in-projection tile
+constexpr int kTlN = 64;    // weight rows (output columns) per in-projection tile (above kTlNarrowB sequences)
+constexpr int kTlNarrowB = 64;  // up to this many sequences (one row tile) the in-projection takes 32-wide tiles
 constexpr int kTlNOut = 32;  // ... per out-projection tile (twice the workgroups: W_o is a quarter of the weights)
 constexpr int kTlK = 64;    // K per LDS stage
 constexpr int kTlWaves = 8;
@@ -440,7 +441,7 @@ struct TileCfg {
     static_assert(kTlM * kPitch * 4 <= kRingBytes, "the epilogue's P tile reuses the ring");
     static_assert(kADma >= 1 && kBDma >= 1, "every wave issues whole copies");
     static_assert(kBBytes % (16 * kBLanes * kTlWaves) == 0 && TN % 32 == 0, "W slice split over the waves");
-    static_assert(kEC * 8 == TN && (MODE == 1 || TN == 64), "epilogue: 8 threads a row; conv tiles are 64 wide");
+    static_assert(kEC * 8 == TN, "epilogue: 8 threads a row");
 };
 
 // Byte offset in a stage of (row r, 16-byte chunk c) of a slice: 8 chunks a
@@ -453,6 +454,8 @@ template <int N>
 struct U16Arr { uint16_t v[N]; };
 template <int N>
 struct U4Arr { u32x4 v[N]; };
+template <typename T, int N>
+struct VArr { T v[N]; };
 
 // NC = conv_k - 1 (MODE 0; 0 for MODE 1); TN weight rows per tile.
 template <int MODE, int NC, int TN>
@@ -470,11 +473,14 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     if (nt >= p.ntiles) return;
     const int m0 = mt * kTlM, n0 = nt * TN;
     const int nk = p.K / kTlK;
-    // K slice order: column tile nt starts at slice nt % nk, so the
+    // K slice order: the tile starts at slice (n0 / 64) % nk, so the
     // workgroups are spread over the slices (and the memory channels that
     // hold them) rather than all on the same one; row tiles of one column
     // tile keep the same order and share its weight slices through L2.
-    const int kstart = nt % nk;
+    // Counted in 64-column blocks whatever the tile width, so every output
+    // sums its K slices in the same order with 32- and 64-wide tiles and
+    // both give bit-identical results.
+    const int kstart = (n0 / 64) % nk;
 
     // Output group of the tile (uniform): q/k/v tiles never straddle groups
     // (their widths are multiples of TN); a and b share the tiles after v.
@@ -488,9 +494,10 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
     const int eb_ld = min(eb, p.B - 1);
 
     // Conv-tile inputs load first and are held through the K loop: the
-    // thread's cached tokens (8 NC bf16, contiguous) and, for threads
-    // t < 64, the conv taps of column n0 + t.
-    u32x4 hold[NC > 0 ? NC : 1];
+    // thread's cached tokens (EC NC bf16, contiguous) and, for threads
+    // t < TN, the conv taps of column n0 + t.
+    using CVec = std::conditional_t<EC == 8, u32x4, u32x2>;  // EC bf16
+    CVec hold[NC > 0 ? NC : 1];
     uint16_t tap[4] = {0, 0, 0, 0};
     int cwidth = 0, ccol = 0;
     uint16_t* cbase = nullptr;
@@ -504,7 +511,12 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
                 const auto crs = buffer_rsrc(cbase, static_cast<uint32_t>(p.B) * cwidth * NC * 2);
                 const uint32_t voff = static_cast<uint32_t>((eb_ld * cwidth + ccol) * NC) * 2;
 #pragma unroll
-                for (int u = 0; u < NC; ++u) hold[u] = buffer_load16(crs, voff, 16 * u);
+                for (int u = 0; u < NC; ++u) {
+                    if constexpr (EC == 8)
+                        hold[u] = buffer_load16(crs, voff, 16 * u);
+                    else
+                        hold[u] = __builtin_amdgcn_raw_buffer_load_b64(crs, voff, 8 * u, 0);
+                }
             }
             if (tid < TN) {
                 const uint16_t* wr = p.conv_w + static_cast<size_t>(n0 + tid) * (NC + 1);
@@ -660,7 +672,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
             }
         }
     } else {
-        // Conv taps of the 8 columns (4 bf16 each, right-aligned: slot 3
+        // Conv taps of the EC columns (4 bf16 each, right-aligned: slot 3
         // multiplies the new token, slots 3 - NC .. 2 the cached tokens,
         // oldest first).
         U16Arr<4 * EC> tp;
@@ -675,7 +687,7 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
         U16Arr<(NC > 0 ? EC * NC : 1)> nwc;
         U16Arr<(NC > 0 ? EC * NC : 1)> old;
         if constexpr (NC > 0) {
-            U4Arr<NC> h;
+            VArr<CVec, NC> h;
 #pragma unroll
             for (int u = 0; u < NC; ++u) h.v[u] = hold[u];
             old = __builtin_bit_cast(U16Arr<EC * NC>, h);
@@ -691,21 +703,23 @@ __global__ __launch_bounds__(kTlThreads) void gdn_decode_tile_kernel(TileParams 
             yv[j] = silu_f(s);
         }
         uint16_t* const d = g == 0 ? p.dst[0] : g == 1 ? p.dst[1] : p.dst[2];
-        *reinterpret_cast<u32x4*>(d + static_cast<size_t>(eb) * cwidth + ccol) =
-            u32x4{pack2_bf16(yv[0], yv[1]), pack2_bf16(yv[2], yv[3]), pack2_bf16(yv[4], yv[5]),
-                  pack2_bf16(yv[6], yv[7])};
+        uint16_t* const dq = d + static_cast<size_t>(eb) * cwidth + ccol;
+        if constexpr (EC == 8)
+            *reinterpret_cast<u32x4*>(dq) = u32x4{pack2_bf16(yv[0], yv[1]), pack2_bf16(yv[2], yv[3]),
+                                                  pack2_bf16(yv[4], yv[5]), pack2_bf16(yv[6], yv[7])};
+        else
+            *reinterpret_cast<u32x2*>(dq) = u32x2{pack2_bf16(yv[0], yv[1]), pack2_bf16(yv[2], yv[3])};
         if constexpr (NC > 0) {
-            const U4Arr<NC> nw = __builtin_bit_cast(U4Arr<NC>, nwc);
-            u32x4* cq = reinterpret_cast<u32x4*>(cbase + (static_cast<size_t>(eb) * cwidth + ccol) * NC);
+            const VArr<CVec, NC> nw = __builtin_bit_cast(VArr<CVec, NC>, nwc);
+            CVec* cq = reinterpret_cast<CVec*>(cbase + (static_cast<size_t>(eb) * cwidth + ccol) * NC);
 #pragma unroll
             for (int u = 0; u < NC; ++u) cq[u] = nw.v[u];
         }
     }
 }
 
-template <int MODE>
-int launch_tile(TileParams& p, hipStream_t st, const char* who) {
-    constexpr int TN = MODE == 1 ? kTlNOut : kTlN;
+template <int MODE, int TN>
+void launch_tile_tn(TileParams& p, hipStream_t st) {
     p.mtiles = (p.B + kTlM - 1) / kTlM;
     p.ntiles = (p.N + TN - 1) / TN;
     const dim3 grid(p.mtiles * ((p.ntiles + 7) / 8) * 8);
@@ -719,6 +733,19 @@ int launch_tile(TileParams& p, hipStream_t st, const char* who) {
             default: hipLaunchKernelGGL((gdn_decode_tile_kernel<0, 3, TN>), grid, dim3(kTlThreads), 0, st, p); break;
         }
     }
+}
+
+// The out-projection always takes 32-wide tiles; the in-projection up to
+// kTlNarrowB sequences (one row tile: 32-wide tiles double its workgroups,
+// which still fit the CUs), 64-wide tiles above.
+template <int MODE>
+int launch_tile(TileParams& p, hipStream_t st, const char* who) {
+    if constexpr (MODE == 1)
+        launch_tile_tn<1, kTlNOut>(p, st);
+    else if (p.B <= kTlNarrowB)
+        launch_tile_tn<0, kTlNOut>(p, st);
+    else
+        launch_tile_tn<0, kTlN>(p, st);
     return gdn_host::check_launch(who);
 }
 
