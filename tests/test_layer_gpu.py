@@ -136,17 +136,19 @@ def test_layer_decode_unfused_path_matches_prefill(dev):
     assert_out_close(torch.cat(ys, 1), y_pre, what="unfused decode vs prefill")
 
 
+@pytest.mark.parametrize("B", [40, 66])
 @pytest.mark.parametrize("ck", [1, 2, 3])
-def test_layer_decode_tiled_conv_widths(dev, ck):
+def test_layer_decode_tiled_conv_widths(dev, ck, B):
     """The tiled step's conv epilogue at conv widths 1..3 (no cache, 1 or 2
-    cached tokens; width 4 is the default elsewhere): decode from a prefill's
-    state against one longer prefill, and the conv caches and x_n history."""
+    cached tokens; width 4 is the default elsewhere), with the in-projection's
+    32-wide tiles (B=40: 4-column conv windows) and 64-wide tiles (B=66):
+    decode from a prefill's state against one longer prefill, and the conv
+    caches and x_n history."""
     _, w = _weights(dev, seed=13)
     w = dict(w)
     for key in ("conv_q", "conv_k", "conv_v"):
         w[key] = w[key][:, :ck].contiguous()
     layer = GDNLayerCustom(w)
-    B = 66
     x = torch.randn(B, 40, 256, generator=torch.Generator().manual_seed(14)).bfloat16().to(dev)
     y_all, st_all = layer.forward(x, return_state=True)
     _, st = layer.forward(x[:, :34], return_state=True)
@@ -283,6 +285,29 @@ def test_layer_config5_decode_matches_oracle(dev, B):
     assert_state_close(st["recurrent"].cpu(), st_ref["recurrent"])
     for key in ("conv_q", "conv_k", "conv_v", "xn"):
         assert_out_close(st[key].cpu(), st_ref[key], what=key)
+
+
+def test_layer_decode_tile_widths_bit_identical(dev):
+    """The tiled step's 32-wide in-projection tiles (B <= 64) against its
+    64-wide tiles (B > 64): 64 sequences stepped alone and as the first 64
+    of 65 give bit-identical outputs, recurrent states, conv caches and x_n
+    history (every output sums its K slices in the same order whatever the
+    tile width; rows of the batch are independent).  Config-5 dims."""
+    g, _, w = _cfg5_weights(dev, seed=17)
+    layer = GDNLayerCustom(w)
+    assert layer.tiled_decode
+    B = 65
+    st = layer.init_decode_state(B)
+    st["recurrent"].copy_(torch.randn(st["recurrent"].shape, generator=g) * 0.02)
+    for key in ("conv_q", "conv_k", "conv_v", "xn"):
+        st[key].copy_(torch.randn(st[key].shape, generator=g) * 0.5)
+    x = torch.randn(B, 1, 2048, generator=g).bfloat16().to(dev)
+    y65, st65 = layer.decode(x, st)
+    y64, st64 = layer.decode(x[:64].contiguous(), {k: v[:64].contiguous() for k, v in st.items()})
+    torch.cuda.synchronize()
+    assert torch.equal(y64, y65[:64]), "32- and 64-wide tiles give different outputs"
+    for key in ("recurrent", "conv_q", "conv_k", "conv_v", "xn"):
+        assert torch.equal(st64[key], st65[key][:64]), key
 
 
 def test_layer_conv_k1_state_hand_off(dev):
