@@ -1985,11 +1985,18 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact,
         // their unequal lengths), below 128 for equal lengths (measured at
         // T = 8192: 128 (sequence, head) pairs run 1.2x faster as one group
         // each than as two, where the map pass and scan cost more than the
-        // idle half of the chip).
+        // idle half of the chip).  Groups of at least 4 chunks; of 2 when
+        // the pairs are one sequence's heads (at most 16 workgroups with one
+        // group) and the sequence is at most 16 chunks, where the map pass's
+        // chain is most of the call (measured at B=1, H=16: T=512 27.7 ->
+        // 23.9 us, T=768 28.9 -> 26.2, T=1024 29.9 -> 28.4; slower at B=2
+        // and 4, and at T=2048).
         const long long base = nheads * s.nvg_out;  // output-pass workgroups (one per CU) with one group
         long long G = 1;
-        if (base < (varlen ? 256 : 128) && max_chunks >= 8)
-            G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / 4);
+        if (base < (varlen ? 256 : 128) && max_chunks >= 8) {
+            const long long min_chunks = (!varlen && base <= 16 && max_chunks <= 16) ? 2 : 4;
+            G = std::min<long long>(std::min<long long>(kMaxGroups, 256 / base), max_chunks / min_chunks);
+        }
         if (exact && G > 1) G = (max_chunks + (max_chunks + G - 1) / G - 1) / ((max_chunks + G - 1) / G);
         s.G = G < 2 ? 1 : static_cast<int>(G);
         // At most half the CUs busy in the output pass (equal lengths, or
