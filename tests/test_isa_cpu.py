@@ -54,3 +54,23 @@ def test_in_proj_dma_wait_covers_only_the_weight_loads(layer_asm, maxsteps):
     assert sum(ln.startswith("buffer_load_dwordx4") for ln in between) == maxsteps, between
     assert all(ln.startswith(("buffer_load_dwordx4", "global_load_ushort", "global_load_dwordx4")) for ln in between)
     assert not any("scratch_" in ln for ln in body), "the kernel spills"
+
+
+def test_tile_kernels_keep_their_ring_waits_and_do_not_spill(layer_asm):
+    """The decode-step tile kernels (gdn_decode_tile_kernel<MODE, NC, TN>)
+    order their LDS ring by explicit vmcnt waits that count the copies a
+    slice issues (two per wave: one of A, one of W, also for 32-wide tiles,
+    whose W copy runs on lanes 0..31 of every wave): vmcnt(6) after the four
+    slots are issued and vmcnt(4) in the loop.  Every instantiation must keep
+    both waits, issue its copies as global_load_lds_dwordx4 only, and not
+    spill (a spill's scratch access inside the loop would shift the count)."""
+    syms = sorted(set(re.findall(r"^(_ZN12_GLOBAL__N_122gdn_decode_tile_kernel\w+):", layer_asm, re.M)))
+    assert len(syms) == 9, syms  # in-projection NC 0..3 x TN 32, 64; out-projection TN 32
+    for sym in syms:
+        body = _function(layer_asm, sym)
+        text = "\n".join(body)
+        assert "scratch_" not in text, f"{sym} spills"
+        waits = re.findall(r"s_waitcnt vmcnt\((\d+)\)", text)
+        assert "6" in waits and "4" in waits, (sym, waits)
+        assert any("global_load_lds_dwordx4" in ln for ln in body), sym
+        assert not any(re.search(r"global_load_lds_dword(x2|x3)?\s", ln) for ln in body), sym
