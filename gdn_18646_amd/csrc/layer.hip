@@ -737,7 +737,9 @@ void launch_tile_tn(TileParams& p, hipStream_t st) {
 
 // The out-projection always takes 32-wide tiles; the in-projection up to
 // kTlNarrowB sequences (one row tile: 32-wide tiles double its workgroups,
-// which still fit the CUs), 64-wide tiles above.
+// which still fit the CUs), 64-wide tiles above (with two row tiles, 32-wide
+// tiles put two workgroups on most CUs and measured ~3 us slower a step at
+// B = 65..128).
 template <int MODE>
 int launch_tile(TileParams& p, hipStream_t st, const char* who) {
     if constexpr (MODE == 1)
