@@ -1986,11 +1986,11 @@ StatePlan plan_state(long long nheads, int dv, long long max_chunks, bool exact,
         // T = 8192: 128 (sequence, head) pairs run 1.2x faster as one group
         // each than as two, where the map pass and scan cost more than the
         // idle half of the chip).  Groups of at least 4 chunks; of 2 when
-        // the pairs are one sequence's heads (at most 16 workgroups with one
-        // group) and the sequence is at most 16 chunks, where the map pass's
-        // chain is most of the call (measured at B=1, H=16: T=512 27.7 ->
-        // 23.9 us, T=768 28.9 -> 26.2, T=1024 29.9 -> 28.4; slower at B=2
-        // and 4, and at T=2048).
+        // there are at most 16 (sequence, head) pairs and at most 16 chunks,
+        // where the map pass's chain is most of the call (measured: B=1,
+        // H=16, T=512 27.7 -> 23.9 us, T=1024 29.9 -> 28.4; H=4, T=900 34.6
+        // -> 30.7; B=2, H=8, T=1024 30.1 -> 28.6; H=2, T=600 33.2 -> 27.4;
+        // slower at 32 or more pairs, and at T=2048).
         const long long base = nheads * s.nvg_out;  // output-pass workgroups (one per CU) with one group
         long long G = 1;
         if (base < (varlen ? 256 : 128) && max_chunks >= 8) {

@@ -145,7 +145,7 @@ def test_prefill_state_composition_full_size(exts, dev):
                                               (2, 1, 2600, 48, True), (4, 16, 650, 128, True),
                                               (1, 16, 4096, 256, False), (1, 2, 2048, 384, True),
                                               (1, 2, 2048, 512, False), (1, 16, 1000, 128, True),
-                                              (1, 16, 512, 128, False)])
+                                              (1, 16, 512, 128, False), (1, 4, 900, 128, True)])
 def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
     """Few (sequence, head) pairs and long sequences: the state pass splits each
     sequence into chunk groups and joins them through the groups' affine maps.
@@ -154,8 +154,9 @@ def test_prefill_chunk_groups(exts, dev, B, H, T, dv, masked):
     several 128-column blocks per head, where the map pass runs psi in blocks
     0 .. dv/128 - 1 and phi in the last block (dv = 256 at the reference's
     H = 16: 8 groups; dv = 384 and 512 at H = 2: 8 groups); and one short
-    sequence's 16 heads in groups of 2 chunks (T = 1000: 8 groups, a ragged
-    last chunk; T = 512: 4 groups).  Slow decay
+    sequence's heads in groups of 2-3 chunks (H = 16, T = 1000: 8 groups, a
+    ragged last chunk; T = 512: 4 groups; H = 4, T = 900: 15 chunks in 5
+    groups).  Slow decay
     (A_log = -8, about 0.9998 per token) so the state carried into each group
     matters: a wrong transition map would show at O(1)."""
     d = synth.prefill_inputs(B, T, H, 128, dv, seed=T + dv, state=True)
