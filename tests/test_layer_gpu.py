@@ -265,14 +265,15 @@ def test_layer_config5_decode_after_prefill(dev):
         assert_out_close(st[key].cpu(), st_all[key].cpu(), what=key)
 
 
-@pytest.mark.parametrize("B", [4, 20, 72, 130])
+@pytest.mark.parametrize("B", [4, 20, 64, 72, 130])
 def test_layer_config5_decode_matches_oracle(dev, B):
     """Config-5 dims: a GPU prefill (T=192) hands its decode state to both the
     GPU layer and the oracle layer's decode (fp32 projection); four steps on
     each, compared step by step (outputs to the scaled 2e-2 bar), then the
     recurrent state (1e-2 relative), conv caches and x_n history.  B=4 runs
-    the skinny fused step, B=20, 72 and 130 the tiled step (one, two and
-    three row tiles)."""
+    the skinny fused step, B=20, 64, 72 and 130 the tiled step (one, one,
+    two and three row tiles; 32-wide in-projection tiles up to 64
+    sequences, 64-wide above)."""
     g, w_cpu, w = _cfg5_weights(dev, seed=12)
     layer, base = GDNLayerCustom(w), GDNLayerBaseline(w_cpu, fp32_proj=True)
     x = torch.randn(B, 196, 2048, generator=g).bfloat16()
